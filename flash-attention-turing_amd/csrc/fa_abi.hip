@@ -1,0 +1,26 @@
+// Shared C-ABI utilities: argument checks and error strings.
+#include <hip/hip_runtime.h>
+
+#include "fa_mi355x.h"
+
+extern "C" int fa_check_tensor(const fa_tensor &t, bool required) {
+    if (!t.ptr) return required ? FA_ERR_INVALID_ARG : FA_OK;
+    if ((reinterpret_cast<uintptr_t>(t.ptr) & 15u) != 0) return FA_ERR_INVALID_ARG;
+    if ((t.batch_stride & 7) || (t.row_stride & 7) || (t.head_stride & 7)) return FA_ERR_INVALID_ARG;
+    return FA_OK;
+}
+
+extern "C" const char *fa_error_string(int code) {
+    switch (code) {
+        case FA_OK:
+            return "success";
+        case FA_ERR_INVALID_ARG:
+            return "fa_mi355x: invalid argument (shape, pointer, stride or alignment)";
+        case FA_ERR_UNSUPPORTED:
+            return "fa_mi355x: unsupported configuration (head_dim must be 64 or 128)";
+        case FA_ERR_WORKSPACE:
+            return "fa_mi355x: missing or too small workspace";
+        default:
+            return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "fa_mi355x: unknown error";
+    }
+}

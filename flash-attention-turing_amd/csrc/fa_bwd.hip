@@ -1,0 +1,498 @@
+// Backward attention for gfx950 (MI355X).
+//
+// Replaces flash_bwd_preprocess_kernel.h:23-96 (D = rowsum(dO * O)),
+// flash_bwd_kernel.h:25-609 (dQ, one workgroup per query block) and
+// :613-1344 (dK/dV, one workgroup per key block), launched by
+// flash_bwd_launch_template.h:69-146, and the GQA reduction that
+// flash_api.cpp:297-307, 338-348 does with expanded per-q-head buffers and
+// torch::sum_out: here the dK/dV workgroup loops over the q-heads of its KV
+// head and accumulates the group in fp32 registers.
+//
+// Math (flash_bwd_kernel.h:417-436, 585-588, 1066-1143, 1317-1319):
+//   P  = exp(scale*S - LSE)     (0 where masked)
+//   dS = P * (dP - D)           with dP = dO V^T, rounded to fp16
+//   dV = P^T dO (P rounded to fp16), dQ = scale * dS K, dK = scale * dS^T Q.
+//
+// dQ kernel: 4 waves x 32 queries; S^T = K Q^T and dP^T = V dO^T put keys on
+// the MFMA M dimension so each lane owns one query (one LSE, one D); dS^T
+// feeds dQ^T += K^T dS^T straight from the accumulators.
+// dK/dV kernel: 4 waves x 32 keys; S = Q K^T and dP = dO V^T put queries on
+// M so P and dS feed dV^T += dO^T P and dK^T += Q^T dS.
+#include "fa_common.h"
+
+namespace fa {
+
+constexpr int kBwdThreads = 256;
+
+// ---------------------------------------------------------------------------
+// Preprocess: dsum[b][h][i] = sum_d fp32(O) * fp32(dO); padding rows get 0.
+template <int HD>
+__global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a) {
+    constexpr int KCH = HD / 8;
+    constexpr int ROWS = kBwdThreads / KCH;  // (row, head) pairs per workgroup
+    const int b = blockIdx.y;
+    const bool packed = a.cu_seqlens_q != nullptr;
+    const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
+    const int t = blockIdx.x * ROWS + threadIdx.x / KCH;  // t = i * nheads + h
+    const int c = threadIdx.x % KCH;
+    const int i = t / a.nheads, h = t - i * a.nheads;
+    if (i >= a.lse_seqlen) return;
+    float acc = 0.f;
+    if (i < si.sq) {
+        const f16 *op = (const f16 *)a.o.ptr + base_off(a.o, packed, b, si.q_start, h) + int64_t(i) * a.o.row_stride;
+        const f16 *dp =
+            (const f16 *)a.dout.ptr + base_off(a.dout, packed, b, si.q_start, h) + int64_t(i) * a.dout.row_stride;
+        const f16x8 ov = as_h8(ldg16(op + 8 * c)), dv = as_h8(ldg16(dp + 8 * c));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += float(ov[j]) * float(dv[j]);
+    }
+#pragma unroll
+    for (int off = KCH / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, KCH);
+    if (c == 0) a.dsum[(int64_t(b) * a.nheads + h) * a.lse_seqlen + i] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// dQ kernel.
+template <int HD>
+struct DqCfg {
+    static constexpr int BM = 128, BN = 64, NT = kBwdThreads, KCH = HD / 8;
+    static constexpr int KN = BN * HD * 2;  // K natural
+    static constexpr int KT = HD * BN * 2;  // K transposed
+    static constexpr int VN = BN * HD * 2;  // V natural
+    static constexpr int STAGE = KN + KT + VN;
+    static constexpr int UNITS = (BN / 4) * KCH;
+    static constexpr int V_LD = BN * KCH / NT;
+};
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks) {
+    using C = DqCfg<HD>;
+    constexpr int BM = C::BM, BN = C::BN, NT = C::NT, KCH = C::KCH;
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hh = lane >> 5;
+    const int bh_count = a.batch * a.nheads;
+    const int bh = blockIdx.x % bh_count;
+    int mb = blockIdx.x / bh_count;
+    if (CAUSAL) mb = num_m_blocks - 1 - mb;
+    const int b = bh / a.nheads, h = bh - b * a.nheads;
+    const int hk = h / (a.nheads / a.nheads_k);
+    const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
+    const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
+    const int sq = si.sq, sk = si.sk;
+    const int m0 = mb * BM;
+    if (m0 >= sq) return;
+
+    const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, h);
+    const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, h);
+    const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, b, si.k_start, hk);
+    const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, b, si.k_start, hk);
+    f16 *dqp = (f16 *)a.dq.ptr + base_off(a.dq, packed_q, b, si.q_start, h);
+    const int64_t lrow = (int64_t(b) * a.nheads + h) * a.lse_seqlen;
+
+    const int causal_off = sk - sq;
+    int n_end = sk;
+    if (CAUSAL) n_end = max(0, min(sk, m0 + BM + causal_off));
+    const int n_blocks = (n_end + BN - 1) / BN;
+    const float cs = a.softmax_scale * kLog2e;
+
+    const int qi = m0 + wave * 32 + col;
+    const bool qv = qi < sq;
+    f16x8 qB[HD / 16], doB[HD / 16];
+#pragma unroll
+    for (int g = 0; g < HD / 16; ++g) {
+        qB[g] = as_h8(qv ? ldg16(qp + int64_t(qi) * a.q.row_stride + 16 * g + 8 * hh) : zero_u4());
+        doB[g] = as_h8(qv ? ldg16(dop + int64_t(qi) * a.dout.row_stride + 16 * g + 8 * hh) : zero_u4());
+    }
+    const float lse2 = qv ? a.lse[lrow + qi] * kLog2e : 0.f;
+    const float dsum = qv ? a.dsum[lrow + qi] : 0.f;
+
+    f32x16 dq[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) dq[i] = zero16();
+
+    u32x4 kreg[4], vreg[C::V_LD];
+    const bool k_thread = tid < C::UNITS;
+    const int um = tid % (BN / 4), uc = tid / (BN / 4);
+    auto load = [&](int nb) {
+        const int n0 = nb * BN;
+        if (k_thread) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = n0 + 4 * um + r;
+                kreg[r] = key < sk ? ldg16(kp + int64_t(key) * a.k.row_stride + 8 * uc) : zero_u4();
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::V_LD; ++i) {
+            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
+            const int key = n0 + row;
+            vreg[i] = key < sk ? ldg16(vp + int64_t(key) * a.v.row_stride + 8 * c) : zero_u4();
+        }
+    };
+    auto store = [&](int buf) {
+        char *kn = smem + buf * C::STAGE;
+        char *kt = kn + C::KN;
+        char *vn = kt + C::KT;
+        if (k_thread) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lds_st16(kn, nat_off<HD>(4 * um + r, uc), kreg[r]);
+            tr_store4<BN>(kt, 4 * um, 8 * uc, kreg[0], kreg[1], kreg[2], kreg[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < C::V_LD; ++i) {
+            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
+            lds_st16(vn, nat_off<HD>(row, c), vreg[i]);
+        }
+    };
+
+    if (n_blocks > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+
+    const int q_lo = m0 + wave * 32;
+    for (int nb = 0; nb < n_blocks; ++nb) {
+        const int buf = nb & 1;
+        if (nb + 1 < n_blocks) load(nb + 1);
+        const int n0 = nb * BN;
+        bool active = true;
+        bool need_mask = n0 + BN > sk;
+        if (CAUSAL) {
+            if (n0 > q_lo + 31 + causal_off) active = false;
+            if (n0 + BN - 1 > q_lo + causal_off) need_mask = true;
+        }
+        if (active) {
+            const char *kn = smem + buf * C::STAGE;
+            const char *kt = kn + C::KN;
+            const char *vn = kt + C::KT;
+            f32x16 s[2], dp[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                s[t] = zero16();
+                dp[t] = zero16();
+                const int row = t * 32 + sigma(col);
+#pragma unroll
+                for (int g = 0; g < HD / 16; ++g) {
+                    s[t] = mfma32(lds_ld16(kn, nat_off<HD>(row, 2 * g + hh)), qB[g], s[t]);
+                    dp[t] = mfma32(lds_ld16(vn, nat_off<HD>(row, 2 * g + hh)), doB[g], dp[t]);
+                }
+            }
+            const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float p = exp2_fast(fmaf(s[t][r], cs, -lse2));
+                    if (need_mask && n0 + t * 32 + acc_lrow(r, hh) > lim) p = 0.f;
+                    s[t][r] = p * (dp[t][r] - dsum);
+                }
+            f16x8 dsB[4];
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) dsB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt) {
+                const int d = dt * 32 + col;
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg)
+                    dq[dt] = mfma32(lds_ld16(kt, tr_off<BN>(d, 2 * gg + hh)), dsB[gg], dq[dt]);
+            }
+        }
+        if (nb + 1 < n_blocks) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (qv) {
+        f16 *row = dqp + int64_t(qi) * a.dq.row_stride;
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                f16x4 v;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[t] = (f16)(dq[dt][4 * a4 + t] * a.softmax_scale);
+                *reinterpret_cast<f16x4 *>(row + dt * 32 + 8 * a4 + 4 * hh) = v;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV kernel.
+template <int HD>
+struct DkvCfg {
+    static constexpr int BN = 128, BM = 64, NT = kBwdThreads, KCH = HD / 8;
+    static constexpr int QN = BM * HD * 2;  // natural [64][HD]
+    static constexpr int QT = HD * BM * 2;  // transposed [HD][64]
+    static constexpr int STAGE = 2 * QN + 2 * QT + 2 * BM * 4;  // Qn Qt dOn dOt lse2 D
+    static constexpr int UNITS = (BM / 4) * KCH;
+};
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
+    using C = DkvCfg<HD>;
+    constexpr int BN = C::BN, BM = C::BM;
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hh = lane >> 5;
+    const int bh_count = a.batch * a.nheads_k;
+    const int bhk = blockIdx.x % bh_count;
+    const int nb = blockIdx.x / bh_count;  // smallest key blocks (most queries) first
+    const int b = bhk / a.nheads_k, hk = bhk - b * a.nheads_k;
+    const int G = a.nheads / a.nheads_k;
+    const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
+    const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
+    const int sq = si.sq, sk = si.sk;
+    const int k0 = nb * BN;
+    if (k0 >= sk) return;
+
+    const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, b, si.k_start, hk);
+    const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, b, si.k_start, hk);
+    f16 *dkp = (f16 *)a.dk.ptr + base_off(a.dk, packed_k, b, si.k_start, hk);
+    f16 *dvp = (f16 *)a.dv.ptr + base_off(a.dv, packed_k, b, si.k_start, hk);
+    const int causal_off = sk - sq;
+    const float cs = a.softmax_scale * kLog2e;
+
+    const int kw0 = k0 + wave * 32;
+    const int key = kw0 + col;
+    const bool kv_ok = key < sk;
+    f16x8 kB[HD / 16], vB[HD / 16];
+#pragma unroll
+    for (int g = 0; g < HD / 16; ++g) {
+        kB[g] = as_h8(kv_ok ? ldg16(kp + int64_t(key) * a.k.row_stride + 16 * g + 8 * hh) : zero_u4());
+        vB[g] = as_h8(kv_ok ? ldg16(vp + int64_t(key) * a.v.row_stride + 16 * g + 8 * hh) : zero_u4());
+    }
+    f32x16 dk[HD / 32], dv[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) {
+        dk[i] = zero16();
+        dv[i] = zero16();
+    }
+
+    // Query blocks that can see this key block, repeated for each q-head of the group.
+    const int m_first = CAUSAL ? max(0, k0 - causal_off) / BM : 0;
+    const int n_qb = max(0, (sq + BM - 1) / BM - m_first);
+    const int total = G * n_qb;
+
+    u32x4 qreg[4], doreg[4];
+    float lreg = 0.f;
+    const bool u_thread = tid < C::UNITS;
+    const int um = tid % (BM / 4), uc = tid / (BM / 4);
+    auto load = [&](int j) {
+        const int hq = hk * G + j / n_qb;
+        const int q0 = (m_first + j % n_qb) * BM;
+        if (u_thread) {
+            const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hq);
+            const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hq);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int q = q0 + 4 * um + r;
+                qreg[r] = q < sq ? ldg16(qp + int64_t(q) * a.q.row_stride + 8 * uc) : zero_u4();
+                doreg[r] = q < sq ? ldg16(dop + int64_t(q) * a.dout.row_stride + 8 * uc) : zero_u4();
+            }
+        }
+        if (tid < 2 * BM) {
+            const int q = q0 + (tid & (BM - 1));
+            const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen;
+            if (tid < BM)
+                lreg = q < sq ? a.lse[lrow + q] * kLog2e : 0.f;
+            else
+                lreg = q < sq ? a.dsum[lrow + q] : 0.f;
+        }
+    };
+    auto store = [&](int buf) {
+        char *qn = smem + buf * C::STAGE;
+        char *qt = qn + C::QN;
+        char *on = qt + C::QT;
+        char *ot = on + C::QN;
+        float *lf = reinterpret_cast<float *>(ot + C::QT);
+        if (u_thread) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                lds_st16(qn, nat_off<HD>(4 * um + r, uc), qreg[r]);
+                lds_st16(on, nat_off<HD>(4 * um + r, uc), doreg[r]);
+            }
+            tr_store4<BM>(qt, 4 * um, 8 * uc, qreg[0], qreg[1], qreg[2], qreg[3]);
+            tr_store4<BM>(ot, 4 * um, 8 * uc, doreg[0], doreg[1], doreg[2], doreg[3]);
+        }
+        if (tid < 2 * BM) lf[tid] = lreg;
+    };
+
+    if (total > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+
+    for (int j = 0; j < total; ++j) {
+        const int buf = j & 1;
+        if (j + 1 < total) load(j + 1);
+        const int q0 = (m_first + j % n_qb) * BM;
+        bool active = true;
+        bool need_mask = q0 + BM > sq || kw0 + 32 > sk;
+        if (CAUSAL) {
+            if (q0 + BM - 1 + causal_off < kw0) active = false;
+            if (kw0 + 31 > q0 + causal_off) need_mask = true;
+        }
+        if (active) {
+            const char *qn = smem + buf * C::STAGE;
+            const char *qt = qn + C::QN;
+            const char *on = qt + C::QT;
+            const char *ot = on + C::QN;
+            const float *lf = reinterpret_cast<const float *>(ot + C::QT);
+            f32x16 s[2], dp[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                s[t] = zero16();
+                dp[t] = zero16();
+                const int row = t * 32 + sigma(col);
+#pragma unroll
+                for (int g = 0; g < HD / 16; ++g) {
+                    s[t] = mfma32(lds_ld16(qn, nat_off<HD>(row, 2 * g + hh)), kB[g], s[t]);
+                    dp[t] = mfma32(lds_ld16(on, nat_off<HD>(row, 2 * g + hh)), vB[g], dp[t]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int ql = t * 32 + acc_lrow(r, hh);
+                    const float l2 = lf[ql], dsum = lf[BM + ql];
+                    float p = exp2_fast(fmaf(s[t][r], cs, -l2));
+                    if (need_mask) {
+                        const int q = q0 + ql;
+                        if (q >= sq || !kv_ok || (CAUSAL && key > q + causal_off)) p = 0.f;
+                    }
+                    s[t][r] = p;
+                    dp[t][r] = p * (dp[t][r] - dsum);
+                }
+            f16x8 pB[4], dsB[4];
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+                dsB[gg] = pack8(dp[gg >> 1], 8 * (gg & 1));
+            }
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt) {
+                const int d = dt * 32 + col;
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) {
+                    dv[dt] = mfma32(lds_ld16(ot, tr_off<BM>(d, 2 * gg + hh)), pB[gg], dv[dt]);
+                    dk[dt] = mfma32(lds_ld16(qt, tr_off<BM>(d, 2 * gg + hh)), dsB[gg], dk[dt]);
+                }
+            }
+        }
+        if (j + 1 < total) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (kv_ok) {
+        f16 *krow = dkp + int64_t(key) * a.dk.row_stride;
+        f16 *vrow = dvp + int64_t(key) * a.dv.row_stride;
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                f16x4 kv4, vv4;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    kv4[t] = (f16)(dk[dt][4 * a4 + t] * a.softmax_scale);
+                    vv4[t] = (f16)dv[dt][4 * a4 + t];
+                }
+                *reinterpret_cast<f16x4 *>(krow + dt * 32 + 8 * a4 + 4 * hh) = kv4;
+                *reinterpret_cast<f16x4 *>(vrow + dt * 32 + 8 * a4 + 4 * hh) = vv4;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers.
+
+static int check_bwd(const fa_bwd_args *p) {
+    if (!p) return FA_ERR_INVALID_ARG;
+    const fa_bwd_args &a = *p;
+    if (a.head_dim != 64 && a.head_dim != 128) return FA_ERR_UNSUPPORTED;
+    if (a.batch < 0 || a.seqlen_q < 0 || a.seqlen_k < 0 || a.nheads <= 0 || a.nheads_k <= 0 ||
+        a.nheads % a.nheads_k != 0 || !a.lse || a.lse_seqlen < a.seqlen_q)
+        return FA_ERR_INVALID_ARG;
+    if (!a.dsum) return FA_ERR_WORKSPACE;
+    return FA_OK;
+}
+
+template <int HD>
+static int launch_preprocess(const fa_bwd_args &a, hipStream_t s) {
+    constexpr int ROWS = kBwdThreads / (HD / 8);
+    const int64_t gx = (int64_t(a.lse_seqlen) * a.nheads + ROWS - 1) / ROWS;
+    if (gx == 0 || a.batch == 0) return FA_OK;
+    hipLaunchKernelGGL(bwd_preprocess_kernel<HD>, dim3(unsigned(gx), unsigned(a.batch)), dim3(kBwdThreads), 0, s,
+                       a);
+    return int(hipGetLastError());
+}
+
+template <int HD, bool CAUSAL>
+static int launch_dq(const fa_bwd_args &a, hipStream_t s) {
+    const int nmb = (a.lse_seqlen + DqCfg<HD>::BM - 1) / DqCfg<HD>::BM;
+    const int64_t grid = int64_t(nmb) * a.batch * a.nheads;
+    if (grid == 0) return FA_OK;
+    hipLaunchKernelGGL((bwd_dq_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a, nmb);
+    return int(hipGetLastError());
+}
+
+template <int HD, bool CAUSAL>
+static int launch_dkdv(const fa_bwd_args &a, hipStream_t s) {
+    // seqlen_k bounds every sequence's key count (max_seqlen_k for varlen).
+    const int nnb = (a.seqlen_k + DkvCfg<HD>::BN - 1) / DkvCfg<HD>::BN;
+    const int64_t grid = int64_t(nnb) * a.batch * a.nheads_k;
+    if (grid == 0) return FA_OK;
+    hipLaunchKernelGGL((bwd_dkdv_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a);
+    return int(hipGetLastError());
+}
+
+}  // namespace fa
+
+extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
+
+static int check_bwd_tensors(const fa_bwd_args *a) {
+    const fa_tensor *ts[] = {&a->q, &a->k, &a->v, &a->o, &a->dout, &a->dq, &a->dk, &a->dv};
+    for (const fa_tensor *t : ts)
+        if (fa_check_tensor(*t, true)) return FA_ERR_INVALID_ARG;
+    return FA_OK;
+}
+
+extern "C" int fa_bwd_preprocess(const fa_bwd_args *args, void *stream) {
+    int rc = fa::check_bwd(args);
+    if (rc) return rc;
+    if ((rc = check_bwd_tensors(args))) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return args->head_dim == 128 ? fa::launch_preprocess<128>(*args, s) : fa::launch_preprocess<64>(*args, s);
+}
+
+extern "C" int fa_bwd_dq(const fa_bwd_args *args, void *stream) {
+    int rc = fa::check_bwd(args);
+    if (rc) return rc;
+    if ((rc = check_bwd_tensors(args))) return rc;
+    const fa_bwd_args &a = *args;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (a.head_dim == 128) return a.causal ? fa::launch_dq<128, true>(a, s) : fa::launch_dq<128, false>(a, s);
+    return a.causal ? fa::launch_dq<64, true>(a, s) : fa::launch_dq<64, false>(a, s);
+}
+
+extern "C" int fa_bwd_dkdv(const fa_bwd_args *args, void *stream) {
+    int rc = fa::check_bwd(args);
+    if (rc) return rc;
+    if ((rc = check_bwd_tensors(args))) return rc;
+    const fa_bwd_args &a = *args;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (a.head_dim == 128) return a.causal ? fa::launch_dkdv<128, true>(a, s) : fa::launch_dkdv<128, false>(a, s);
+    return a.causal ? fa::launch_dkdv<64, true>(a, s) : fa::launch_dkdv<64, false>(a, s);
+}
+
+extern "C" int fa_bwd(const fa_bwd_args *args, void *stream) {
+    int rc = fa_bwd_preprocess(args, stream);
+    if (rc) return rc;
+    rc = fa_bwd_dq(args, stream);
+    if (rc) return rc;
+    return fa_bwd_dkdv(args, stream);
+}

@@ -1,0 +1,165 @@
+// Device helpers shared by the gfx950 attention kernels.
+//
+// MFMA conventions (v_mfma_f32_32x32x16_f16, wave64):
+//   A operand (32 x 16): lane l supplies row l%32, K slots 8*(l/32)+0..7
+//   B operand (16 x 32): lane l supplies column l%32, K slots 8*(l/32)+0..7
+//   C/D (32 x 32, 16 fp32 per lane): lane l holds column l%32 and rows
+//       8*(r/4) + 4*(l/32) + r%4 for accumulator r = 0..15.
+//
+// Chaining an accumulator tile into the K dimension of the next MFMA:
+// the rows of a C tile live in a lane in two runs (r = 0..7, r = 8..15).  If
+// the first GEMM's operand that supplies those rows is loaded with the row
+// permutation sigma (swap bits 2 and 3 of the row index), accumulator
+// r of lane half h holds logical row 16*(r/8) + 8*h + r%8.  Accumulators
+// 8g..8g+7 of a lane are then exactly the 8 consecutive logical rows that
+// lane supplies in K step g of a following MFMA, so S^T / P^T / dS^T tiles
+// feed the PV, dV, dK and dQ products with no data movement (a C tile is
+// the B operand of the same matrix, and the A operand of its transpose).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fa_mi355x.h"
+
+namespace fa {
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma32(const f16x8 a, const f16x8 b, const f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+    f32x16 z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    return z;
+}
+
+// Row permutation applied when loading rows that a later MFMA consumes along K.
+__device__ __forceinline__ int sigma(int i) {
+    return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+// Logical row (0..31) of accumulator r in lane half h for a sigma-loaded tile.
+__device__ __forceinline__ int acc_lrow(int r, int h) { return 16 * (r >> 3) + 8 * h + (r & 7); }
+// Natural row of accumulator r in lane half h (no permutation at load).
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------
+// LDS tiles.  All tiles are addressed in 16-byte chunks with an XOR swizzle on
+// the low 3 bits of the chunk index so that the MFMA operand reads (32 rows,
+// same logical chunk) and the staging writes are bank-conflict free.
+
+// Natural tile [rows][D] fp16: operand reads touch rows sigma(0..31).
+__device__ __forceinline__ int swz_nat(int row) {
+    const int r = row & 3;
+    return ((row >> 2) & 7) ^ ((r & 1) | ((r & 2) << 1));
+}
+template <int D>
+__device__ __forceinline__ int nat_off(int row, int chunk) {
+    return row * (D * 2) + ((chunk ^ swz_nat(row)) << 4);
+}
+// Transposed tile [X][R] fp16 (element (x, k) = source row k, column x):
+// operand reads touch x = 0..31 consecutive at one key chunk.
+template <int R>
+__device__ __forceinline__ int tr_off(int x, int kchunk) {
+    return x * (R * 2) + ((kchunk ^ (x & (R / 8 - 1) & 7)) << 4);
+}
+
+__device__ __forceinline__ f16x8 lds_ld16(const char *base, int off) {
+    return *reinterpret_cast<const f16x8 *>(base + off);
+}
+__device__ __forceinline__ void lds_st16(char *base, int off, const u32x4 v) {
+    *reinterpret_cast<u32x4 *>(base + off) = v;
+}
+
+// Write 4 source rows (k0..k0+3, 8 columns x0..x0+7 each, one u32x4 per row)
+// into a transposed tile [X][R]: column x0+j receives the 4 halves of rows
+// k0..k0+3 as one 8-byte store.
+template <int R>
+__device__ __forceinline__ void tr_store4(char *base, int k0, int x0, const u32x4 r0, const u32x4 r1,
+                                          const u32x4 r2, const u32x4 r3) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t a = r0[p], b = r1[p], c = r2[p], d = r3[p];
+        u32x2 lo, hi;
+        lo[0] = (a & 0xffffu) | (b << 16);
+        lo[1] = (c & 0xffffu) | (d << 16);
+        hi[0] = (a >> 16) | (b & 0xffff0000u);
+        hi[1] = (c >> 16) | (d & 0xffff0000u);
+        const int xa = x0 + 2 * p, xb = xa + 1;
+        *reinterpret_cast<u32x2 *>(base + tr_off<R>(xa, k0 >> 3) + ((k0 & 4) << 1)) = lo;
+        *reinterpret_cast<u32x2 *>(base + tr_off<R>(xb, k0 >> 3) + ((k0 & 4) << 1)) = hi;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Global memory.
+
+__device__ __forceinline__ u32x4 ldg16(const f16 *p) { return *reinterpret_cast<const u32x4 *>(p); }
+__device__ __forceinline__ u32x4 zero_u4() {
+    u32x4 z;
+    z[0] = z[1] = z[2] = z[3] = 0u;
+    return z;
+}
+__device__ __forceinline__ f16x8 as_h8(const u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+__device__ __forceinline__ u32x4 neg_h8(const u32x4 v) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = v[i] ^ 0x80008000u;
+    return r;
+}
+
+// 8 fp32 accumulators -> one fp16x8 MFMA operand (round to nearest even).
+__device__ __forceinline__ f16x8 pack8(const f32x16 &acc, int base) {
+    f16x8 r;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r[t] = (f16)acc[base + t];
+    return r;
+}
+
+// Per-batch extents of a dense or packed (varlen) batch.
+struct SeqInfo {
+    int q_start, sq, k_start, sk;
+};
+
+__device__ __forceinline__ SeqInfo seq_info(int b, int seqlen_q, int seqlen_k, const int32_t *cu_q,
+                                            const int32_t *cu_k, const int32_t *seqused_k, int seqused_add) {
+    SeqInfo s;
+    s.q_start = 0;
+    s.sq = seqlen_q;
+    s.k_start = 0;
+    s.sk = seqlen_k;
+    if (cu_q) {
+        s.q_start = cu_q[b];
+        s.sq = cu_q[b + 1] - s.q_start;
+    }
+    if (cu_k) {
+        s.k_start = cu_k[b];
+        s.sk = cu_k[b + 1] - s.k_start;
+    } else if (seqused_k) {
+        s.sk = seqused_k[b] + seqused_add;
+    }
+    return s;
+}
+
+// Element offset of (batch b / packed row start, head) in a strided tensor.
+__device__ __forceinline__ int64_t base_off(const fa_tensor &t, bool packed, int b, int row_start, int head) {
+    return (packed ? int64_t(row_start) * t.row_stride : int64_t(b) * t.batch_stride) +
+           int64_t(head) * t.head_stride;
+}
+
+}  // namespace fa

@@ -1,0 +1,267 @@
+// Forward attention for gfx950 (MI355X).
+//
+// Replaces the reference forward (csrc/flash_attn/src/flash_fwd_kernel.h:23-711,
+// flash_fwd_launch_template.h:9-118).  Semantics kept: fp16 Q/K/V, fp32
+// accumulation, scale applied to the fp32 scores, bottom-right causal mask
+// (mask.h:52-104), GQA head mapping (fwd_kernel.h:76), varlen offsets and
+// seqused_k (block_info.h:4-36), P rounded to fp16 before the PV product
+// (fwd_kernel.h:415), O = 0 and LSE = 0 for a row with no visible key
+// (fwd_kernel.h:616-662).
+//
+// Design: one workgroup = 4 waves = 128 queries of one (batch, head); each
+// wave owns 32 queries.  The wave computes S^T = K Q^T (keys on the MFMA M
+// dimension) so each lane holds one query column and 32 keys of a 64-key
+// block: the row max needs one cross-half exchange and the row sum none.
+// Q^T stays in registers as the B operand; K (natural) and V (transposed)
+// tiles are double-buffered in LDS with one barrier per block; P^T feeds the
+// O^T += V^T P^T MFMAs directly from the accumulators (see fa_common.h).
+#include "fa_common.h"
+
+namespace fa {
+
+template <int HD>
+struct FwdCfg {
+    static constexpr int BM = 128;               // queries per workgroup
+    static constexpr int BN = 64;                // keys per block
+    static constexpr int NT = 256;               // threads
+    static constexpr int KCH = HD / 8;           // 16-byte chunks per row
+    static constexpr int K_BYTES = BN * HD * 2;  // natural K tile
+    static constexpr int V_BYTES = HD * BN * 2;  // transposed V tile
+    static constexpr int STAGE = K_BYTES + V_BYTES;
+    static constexpr int K_LD = BN * KCH / NT;   // K chunks per thread
+    static constexpr int V_UNITS = (BN / 4) * KCH;
+};
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
+    using C = FwdCfg<HD>;
+    constexpr int BM = C::BM, BN = C::BN, NT = C::NT, KCH = C::KCH;
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hh = lane >> 5;
+
+    // Causal blocks are issued heaviest (largest m block) first.
+    const int bh_count = a.batch * a.nheads;
+    const int bh = blockIdx.x % bh_count;
+    int mb = blockIdx.x / bh_count;
+    if (CAUSAL) mb = num_m_blocks - 1 - mb;
+    const int b = bh / a.nheads, h = bh - b * a.nheads;
+    const int hk = h / (a.nheads / a.nheads_k);
+
+    const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
+    const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k,
+                                a.seqused_k_add);
+    const int sq = si.sq, sk = si.sk;
+    const int m0 = mb * BM;
+    float *lse_row = a.lse + (int64_t(b) * a.nheads + h) * a.lse_seqlen;
+    if (m0 >= sq) {
+        // Rows past this sequence's length: LSE padding is 0 (flash_api.cpp:388).
+        for (int i = m0 + tid; i < m0 + BM && i < a.lse_seqlen; i += NT) lse_row[i] = 0.f;
+        return;
+    }
+    const int kb = a.k_batch_idx ? a.k_batch_idx[b] : b;
+    const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, h);
+    const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, kb, si.k_start, hk);
+    const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, kb, si.k_start, hk);
+    f16 *op = (f16 *)a.o.ptr + base_off(a.o, packed_q, b, si.q_start, h);
+    const int64_t qrs = a.q.row_stride, krs = a.k.row_stride, vrs = a.v.row_stride, ors = a.o.row_stride;
+
+    const int causal_off = sk - sq;  // key j visible to query i iff j <= i + causal_off
+    int n_end = sk;
+    if (CAUSAL) n_end = max(0, min(sk, m0 + BM + causal_off));
+    const int n_blocks = (n_end + BN - 1) / BN;
+
+    // Negative scales are folded into Q's sign so that the exp argument uses |scale|.
+    const bool neg = a.softmax_scale < 0.f;
+    const float cscale = fabsf(a.softmax_scale) * kLog2e;
+
+    // Q^T as the B operand: lane (query col, half hh), K step g covers d = 16g + 8hh + 0..7.
+    const int qi = m0 + wave * 32 + col;
+    f16x8 qB[HD / 16];
+#pragma unroll
+    for (int g = 0; g < HD / 16; ++g) {
+        u32x4 v = zero_u4();
+        if (qi < sq) v = ldg16(qp + int64_t(qi) * qrs + 16 * g + 8 * hh);
+        if (neg) v = neg_h8(v);
+        qB[g] = as_h8(v);
+    }
+
+    f32x16 o[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
+    float m_t = -INFINITY;  // running max of scale*log2(e)*S for this lane's query
+    float l_p = 0.f;        // partial row sum over this lane half's keys
+
+    u32x4 kreg[C::K_LD];
+    u32x4 vreg[4];
+    const bool v_thread = tid < C::V_UNITS;
+    const int vm = tid % (BN / 4), vc = tid / (BN / 4);
+
+    auto load_kv = [&](int nb) {
+        const int n0 = nb * BN;
+#pragma unroll
+        for (int i = 0; i < C::K_LD; ++i) {
+            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
+            const int key = n0 + row;
+            kreg[i] = key < sk ? ldg16(kp + int64_t(key) * krs + 8 * c) : zero_u4();
+        }
+        if (v_thread) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = n0 + 4 * vm + r;
+                vreg[r] = key < sk ? ldg16(vp + int64_t(key) * vrs + 8 * vc) : zero_u4();
+            }
+        }
+    };
+    auto store_kv = [&](int buf) {
+        char *ks = smem + buf * C::STAGE;
+        char *vs = ks + C::K_BYTES;
+#pragma unroll
+        for (int i = 0; i < C::K_LD; ++i) {
+            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
+            lds_st16(ks, nat_off<HD>(row, c), kreg[i]);
+        }
+        if (v_thread) tr_store4<BN>(vs, 4 * vm, 8 * vc, vreg[0], vreg[1], vreg[2], vreg[3]);
+    };
+
+    if (n_blocks > 0) {
+        load_kv(0);
+        store_kv(0);
+    }
+    __syncthreads();
+
+    const int q_lo = m0 + wave * 32;
+    for (int nb = 0; nb < n_blocks; ++nb) {
+        const int buf = nb & 1;
+        if (nb + 1 < n_blocks) load_kv(nb + 1);
+        const int n0 = nb * BN;
+
+        bool active = true;
+        bool need_mask = n0 + BN > sk;
+        if (CAUSAL) {
+            if (n0 > q_lo + 31 + causal_off) active = false;
+            if (n0 + BN - 1 > q_lo + causal_off) need_mask = true;
+        }
+        if (active) {
+            const char *ks = smem + buf * C::STAGE;
+            const char *vs = ks + C::K_BYTES;
+            f32x16 s[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                s[kt] = zero16();
+                const int row = kt * 32 + sigma(col);
+#pragma unroll
+                for (int g = 0; g < HD / 16; ++g) s[kt] = mfma32(lds_ld16(ks, nat_off<HD>(row, 2 * g + hh)), qB[g], s[kt]);
+            }
+
+            float mx = -INFINITY;
+            if (need_mask) {
+                const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (n0 + kt * 32 + acc_lrow(r, hh) > lim) s[kt][r] = -INFINITY;
+            }
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
+            const float m_new = fmaxf(m_t, mx_t);
+            const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            float rs = 0.f;
+            if (need_mask) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float x = s[kt][r];
+                        const float p = x == -INFINITY ? 0.f : exp2_fast(fmaf(x, cscale, -m_use));
+                        s[kt][r] = p;
+                        rs += p;
+                    }
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float p = exp2_fast(fmaf(s[kt][r], cscale, -m_use));
+                        s[kt][r] = p;
+                        rs += p;
+                    }
+            }
+            l_p = l_p * alpha + rs;
+            m_t = m_new;
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+
+            f16x8 pB[4];
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt) {
+                const int d = dt * 32 + col;
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(lds_ld16(vs, tr_off<BN>(d, 2 * gg + hh)), pB[gg], o[dt]);
+            }
+        }
+        if (nb + 1 < n_blocks) store_kv(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
+    const float l_tot = l_p + __shfl_xor(l_p, 32);
+    if (qi < sq) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        f16 *orow = op + int64_t(qi) * ors;
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                f16x4 v;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[t] = (f16)(o[dt][4 * a4 + t] * inv);
+                *reinterpret_cast<f16x4 *>(orow + dt * 32 + 8 * a4 + 4 * hh) = v;
+            }
+        if (hh == 0) lse_row[qi] = l_tot > 0.f ? (m_t + log2_fast(l_tot)) * kLn2 : 0.f;
+    } else if (hh == 0 && qi < a.lse_seqlen) {
+        lse_row[qi] = 0.f;
+    }
+}
+
+template <int HD, bool CAUSAL>
+static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
+    const int num_m_blocks = (a.lse_seqlen + FwdCfg<HD>::BM - 1) / FwdCfg<HD>::BM;
+    const int64_t grid = int64_t(num_m_blocks) * a.batch * a.nheads;
+    if (grid == 0) return FA_OK;
+    if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(FwdCfg<HD>::NT), 0, stream, a,
+                       num_m_blocks);
+    return int(hipGetLastError());
+}
+
+}  // namespace fa
+
+extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
+
+extern "C" int fa_fwd(const fa_fwd_args *args, void *stream) {
+    if (!args) return FA_ERR_INVALID_ARG;
+    const fa_fwd_args &a = *args;
+    if (a.head_dim != 64 && a.head_dim != 128) return FA_ERR_UNSUPPORTED;
+    if (a.batch < 0 || a.seqlen_q < 0 || a.seqlen_k < 0 || a.nheads <= 0 || a.nheads_k <= 0 ||
+        a.nheads % a.nheads_k != 0 || !a.lse || a.lse_seqlen < a.seqlen_q)
+        return FA_ERR_INVALID_ARG;
+    if (fa_check_tensor(a.q, true) || fa_check_tensor(a.k, true) || fa_check_tensor(a.v, true) ||
+        fa_check_tensor(a.o, true))
+        return FA_ERR_INVALID_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (a.head_dim == 128)
+        return a.causal ? fa::launch_fwd<128, true>(a, s) : fa::launch_fwd<128, false>(a, s);
+    return a.causal ? fa::launch_fwd<64, true>(a, s) : fa::launch_fwd<64, false>(a, s);
+}

@@ -1,0 +1,415 @@
+// KV-cache attention for gfx950 (MI355X): in-place append, split-KV partial
+// attention over contiguous / remapped / paged caches, log-sum-exp combine.
+//
+// Replaces csrc/flash_attn/src/kvcache_native.cu: paged_append_kernel
+// (:782-871), the contiguous append loop of flash_api.cpp:643-654, the split
+// kernels (:148-674) and kvcache_combine_kernel (:676-729).  Semantics kept:
+// attention over L = cache_seqlens[b] + seqlen_new keys; split s of S covers
+// [L*s/S, L*(s+1)/S) (:191-192); causal keeps key j for query row i iff
+// j <= i + L - seqlen_q (:347); GQA kv_head = head / (h/hk) (:341); an empty
+// split has LSE -inf and output 0 (:355-372); the combine weights are
+// exp(lse_s - lse_total) and a row with no key gets O = 0, LSE = 0 (:697-727);
+// probabilities stay fp32 through the PV product (:599, :636-672).
+//
+// Design: one workgroup per (batch, KV head, split, 32-row tile) where the
+// rows are the q-heads of the GQA group times the query positions, so every
+// K/V byte of the split is read once.  The keys of the split are walked in
+// 32-key tiles aligned to absolute positions (a tile never straddles a page:
+// pages are multiples of 256 tokens), tile t going to wave t % 4.  Each wave
+// keeps its own online softmax state and stages its tile through a private
+// LDS region (K natural, V transposed), so the main loop has no workgroup
+// barrier; the next tile's loads are in flight while the current tile is
+// computed.  The four waves merge their partial states through LDS at the end.
+// Paged, remapped and contiguous caches take the same tile order and the same
+// arithmetic, so their results are bit-identical for the same logical cache.
+#include <algorithm>
+
+#include "fa_common.h"
+
+namespace fa {
+
+constexpr int kKvThreads = 256;
+constexpr int kKvWaves = 4;
+constexpr int kTile = 32;  // keys per wave tile
+
+__device__ __forceinline__ const f16 *kv_row_ptr(const fa_tensor &t, const fa_kvcache_args &a, int b, int cache_row,
+                                                 int hk, int pos) {
+    // Element pointer of token `pos` (logical) of sequence b, head hk.
+    int64_t off;
+    if (a.block_table) {
+        const int page = a.page_block_size;
+        const int blk = a.block_table[int64_t(b) * a.block_table_stride + pos / page];
+        off = int64_t(blk) * t.batch_stride + int64_t(pos % page) * t.row_stride;
+    } else {
+        off = int64_t(cache_row) * t.batch_stride + int64_t(pos) * t.row_stride;
+    }
+    return (const f16 *)t.ptr + off + int64_t(hk) * t.head_stride;
+}
+
+// ---------------------------------------------------------------------------
+// Append: one thread per 16-byte chunk of k_new / v_new.
+template <int HD>
+__global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a) {
+    constexpr int KCH = HD / 8;
+    const int64_t total = int64_t(a.batch) * a.seqlen_new * a.nheads_k * KCH;
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int c = int(idx % KCH);
+    int64_t rest = idx / KCH;
+    const int hk = int(rest % a.nheads_k);
+    rest /= a.nheads_k;
+    const int t = int(rest % a.seqlen_new);
+    const int b = int(rest / a.seqlen_new);
+    const int pos = a.cache_seqlens[b] + t;
+    const int cache_row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
+    const f16 *ks = (const f16 *)a.k_new.ptr + int64_t(b) * a.k_new.batch_stride + int64_t(t) * a.k_new.row_stride +
+                    int64_t(hk) * a.k_new.head_stride + 8 * c;
+    const f16 *vs = (const f16 *)a.v_new.ptr + int64_t(b) * a.v_new.batch_stride + int64_t(t) * a.v_new.row_stride +
+                    int64_t(hk) * a.v_new.head_stride + 8 * c;
+    f16 *kd = const_cast<f16 *>(kv_row_ptr(a.k_cache, a, b, cache_row, hk, pos)) + 8 * c;
+    f16 *vd = const_cast<f16 *>(kv_row_ptr(a.v_cache, a, b, cache_row, hk, pos)) + 8 * c;
+    *reinterpret_cast<u32x4 *>(kd) = ldg16(ks);
+    *reinterpret_cast<u32x4 *>(vd) = ldg16(vs);
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV partial attention.
+template <int HD>
+struct KvCfg {
+    static constexpr int KCH = HD / 8;
+    static constexpr int KN = kTile * HD * 2;  // natural K tile (per wave)
+    static constexpr int VT = HD * kTile * 2;  // transposed V tile (per wave)
+    static constexpr int WAVE_LDS = KN + VT;   // also holds HD x 32 fp32 at the merge (same size)
+    static constexpr int K_LD = kTile * KCH / 64;        // K chunks per lane
+    static constexpr int V_UNITS = (kTile / 4) * KCH;    // 4-row units per tile
+    static constexpr int V_LD = V_UNITS / 64;            // units per lane
+};
+
+template <int HD>
+__global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a, const int row_tiles) {
+    using C = KvCfg<HD>;
+    constexpr int KCH = C::KCH;
+    __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hh = lane >> 5;
+    const int split = blockIdx.y;
+    int rest = blockIdx.x;
+    const int rt = rest % row_tiles;
+    rest /= row_tiles;
+    const int hk = rest % a.nheads_k;
+    const int b = rest / a.nheads_k;
+    const int G = a.nheads / a.nheads_k;
+    const int R = G * a.seqlen_q;  // rows of this (batch, kv head): row = qpos * G + g
+
+    const int L = a.cache_seqlens[b] + a.seqlen_new;
+    const int S = a.num_splits;
+    const int s0 = int((int64_t(L) * split) / S), s1 = int((int64_t(L) * (split + 1)) / S);
+    const int cache_row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
+
+    // This lane's query row.
+    const int row = rt * 32 + col;
+    const bool row_ok = row < R;
+    const int qpos = row_ok ? row / G : 0;
+    const int hq = hk * G + (row_ok ? row % G : 0);
+    const int lim = a.causal ? qpos + L - a.seqlen_q : L - 1;  // last visible key
+
+    const bool neg = a.softmax_scale < 0.f;
+    const float cscale = fabsf(a.softmax_scale) * kLog2e;
+    f16x8 qB[HD / 16];
+    {
+        const f16 *qp = (const f16 *)a.q.ptr + int64_t(b) * a.q.batch_stride + int64_t(qpos) * a.q.row_stride +
+                        int64_t(hq) * a.q.head_stride;
+#pragma unroll
+        for (int g = 0; g < HD / 16; ++g) {
+            u32x4 v = row_ok ? ldg16(qp + 16 * g + 8 * hh) : zero_u4();
+            if (neg) v = neg_h8(v);
+            qB[g] = as_h8(v);
+        }
+    }
+
+    f32x16 o[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
+    float m_t = -INFINITY, l_p = 0.f;
+
+    char *ks = smem + wave * C::WAVE_LDS;
+    char *vs = ks + C::KN;
+    const int t_first = s0 / kTile;
+    const int t_last = s1 > s0 ? (s1 - 1) / kTile : t_first - 1;
+
+    u32x4 kreg[C::K_LD], vreg[4 * C::V_LD];
+    auto load = [&](int t) {
+        const int p0 = t * kTile;
+        const f16 *kb = kv_row_ptr(a.k_cache, a, b, cache_row, hk, p0);
+        const f16 *vb = kv_row_ptr(a.v_cache, a, b, cache_row, hk, p0);
+        const int64_t krs = a.k_cache.row_stride, vrs = a.v_cache.row_stride;
+#pragma unroll
+        for (int i = 0; i < C::K_LD; ++i) {
+            const int idx = lane + 64 * i, r = idx / KCH, c = idx % KCH;
+            kreg[i] = p0 + r < L ? ldg16(kb + int64_t(r) * krs + 8 * c) : zero_u4();
+        }
+#pragma unroll
+        for (int i = 0; i < C::V_LD; ++i) {
+            const int u = lane + 64 * i, m = u % (kTile / 4), c = u / (kTile / 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                vreg[4 * i + r] = p0 + 4 * m + r < L ? ldg16(vb + int64_t(4 * m + r) * vrs + 8 * c) : zero_u4();
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int i = 0; i < C::K_LD; ++i) {
+            const int idx = lane + 64 * i, r = idx / KCH, c = idx % KCH;
+            lds_st16(ks, nat_off<HD>(r, c), kreg[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < C::V_LD; ++i) {
+            const int u = lane + 64 * i, m = u % (kTile / 4), c = u / (kTile / 4);
+            tr_store4<kTile>(vs, 4 * m, 8 * c, vreg[4 * i], vreg[4 * i + 1], vreg[4 * i + 2], vreg[4 * i + 3]);
+        }
+    };
+
+    int t = t_first + wave;
+    if (t <= t_last) load(t);
+    for (; t <= t_last; t += kKvWaves) {
+        store();
+        __builtin_amdgcn_wave_barrier();
+        if (t + kKvWaves <= t_last) load(t + kKvWaves);
+        const int p0 = t * kTile;
+        f32x16 s = zero16();
+        {
+            const int r = sigma(col);
+#pragma unroll
+            for (int g = 0; g < HD / 16; ++g) s = mfma32(lds_ld16(ks, nat_off<HD>(r, 2 * g + hh)), qB[g], s);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = p0 + acc_lrow(r, hh);
+            if (key < s0 || key >= s1 || key > lim) s[r] = -INFINITY;
+            mx = fmaxf(mx, s[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
+        const float m_new = fmaxf(m_t, mx_t);
+        const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        float rs = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = s[r] == -INFINITY ? 0.f : exp2_fast(fmaf(s[r], cscale, -m_use));
+            s[r] = p;
+            rs += p;
+        }
+        l_p = l_p * alpha + rs;
+        m_t = m_new;
+        // P stays fp32-accurate through the product: P = hi + lo with both halves fp16.
+        f16x8 ph[2], pl[2];
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float p = s[8 * gg + u];
+                const f16 hi = (f16)p;
+                ph[gg][u] = hi;
+                pl[gg][u] = (f16)(p - float(hi));
+            }
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            const int d = dt * 32 + col;
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) {
+                const f16x8 va = lds_ld16(vs, tr_off<kTile>(d, 2 * gg + hh));
+                o[dt] = mfma32(va, ph[gg], o[dt]);
+                o[dt] = mfma32(va, pl[gg], o[dt]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // Merge the four waves: each publishes (m, l) per row and its O^T tile.
+    const float l_w = l_p + __shfl_xor(l_p, 32);
+    float *mrow = reinterpret_cast<float *>(smem + kKvWaves * C::WAVE_LDS);
+    float *lrow = mrow + kKvWaves * 32;
+    __syncthreads();  // every wave is done with its tile region
+    float *ow = reinterpret_cast<float *>(smem + wave * C::WAVE_LDS);  // [HD][32] fp32
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ow[(dt * 32 + acc_row(r, hh)) * 32 + col] = o[dt][r];
+    if (hh == 0) {
+        mrow[wave * 32 + col] = m_t;
+        lrow[wave * 32 + col] = l_w;
+    }
+    __syncthreads();
+
+    const int rows_here = min(32, R - rt * 32);
+    const int nrow_all = a.batch * a.nheads * a.seqlen_q;
+    for (int e = tid; e < rows_here * HD; e += kKvThreads) {
+        const int c = e / HD, d = e % HD;
+        float mstar = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kKvWaves; ++w) mstar = fmaxf(mstar, mrow[w * 32 + c]);
+        float lsum = 0.f, acc = 0.f;
+        if (mstar != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kKvWaves; ++w) {
+                const float mw = mrow[w * 32 + c];
+                const float sc = mw == -INFINITY ? 0.f : exp2_fast(mw - mstar);
+                lsum += lrow[w * 32 + c] * sc;
+                acc += reinterpret_cast<const float *>(smem + w * C::WAVE_LDS)[d * 32 + c] * sc;
+            }
+        }
+        const bool live = lsum > 0.f;
+        const float outv = live ? acc / lsum : 0.f;
+        const float lse = live ? (mstar + log2_fast(lsum)) * kLn2 : -INFINITY;
+        const int r = rt * 32 + c;
+        const int qp = r / G, h = hk * G + r % G;
+        const int64_t orow = (int64_t(b) * a.nheads + h) * a.seqlen_q + qp;  // (batch, head, qpos)
+        if (S == 1) {
+            f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
+                      int64_t(h) * a.o.head_stride;
+            op[d] = (f16)outv;
+            if (d == 0) a.lse[orow] = live ? lse : 0.f;
+        } else {
+            a.out_accum[(int64_t(split) * nrow_all + orow) * HD + d] = outv;
+            if (d == 0) a.lse_accum[int64_t(split) * nrow_all + orow] = lse;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Combine: one wave per (batch, head, qpos) row.
+template <int HD>
+__global__ __launch_bounds__(256) void kv_combine_kernel(const fa_kvcache_args a) {
+    const int nrow = a.batch * a.nheads * a.seqlen_q;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= nrow) return;
+    const int S = a.num_splits;
+    float lmax = -INFINITY;
+    for (int s = 0; s < S; ++s) lmax = fmaxf(lmax, a.lse_accum[int64_t(s) * nrow + r]);
+    float wsum = 0.f;
+    if (lmax != -INFINITY)
+        for (int s = 0; s < S; ++s) wsum += expf(a.lse_accum[int64_t(s) * nrow + r] - lmax);
+    const bool live = lmax != -INFINITY && wsum > 0.f;
+    const float ltot = live ? lmax + logf(wsum) : -INFINITY;
+    const int qp = r % a.seqlen_q;
+    const int bh = r / a.seqlen_q;
+    const int h = bh % a.nheads, b = bh / a.nheads;
+    f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
+              int64_t(h) * a.o.head_stride;
+    for (int d = lane; d < HD; d += 64) {
+        float acc = 0.f;
+        if (live)
+            for (int s = 0; s < S; ++s)
+                acc += expf(a.lse_accum[int64_t(s) * nrow + r] - ltot) * a.out_accum[(int64_t(s) * nrow + r) * HD + d];
+        op[d] = (f16)acc;
+    }
+    if (lane == 0) a.lse[r] = live ? ltot : 0.f;
+}
+
+static int check_kv(const fa_kvcache_args *p) {
+    if (!p) return FA_ERR_INVALID_ARG;
+    const fa_kvcache_args &a = *p;
+    if (a.head_dim != 64 && a.head_dim != 128) return FA_ERR_UNSUPPORTED;
+    if (a.batch < 0 || a.seqlen_q < 0 || a.nheads <= 0 || a.nheads_k <= 0 || a.nheads % a.nheads_k != 0 ||
+        a.seqlen_new < 0 || a.num_splits < 1 || !a.cache_seqlens || !a.lse)
+        return FA_ERR_INVALID_ARG;
+    if (a.block_table && (a.page_block_size <= 0 || a.page_block_size % kTile != 0)) return FA_ERR_INVALID_ARG;
+    if (a.block_table && a.cache_batch_idx) return FA_ERR_INVALID_ARG;
+    return FA_OK;
+}
+
+}  // namespace fa
+
+extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
+
+extern "C" int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seqlen_q, int batch,
+                                int nheads, int nheads_k, int num_cus) {
+    // An explicit request is honoured (kvcache_native.cu:922-924).  Otherwise
+    // split only when the (batch, kv head, row tile) workgroups cannot fill
+    // two rounds of the chip, and keep at least 512 keys per split.
+    (void)head_dim;
+    if (requested > 0) return requested;
+    if (batch <= 0 || nheads_k <= 0 || nheads <= 0) return 1;
+    const int rows = (nheads / nheads_k) * seqlen_q;
+    const int64_t wgs = int64_t(batch) * nheads_k * ((rows + 31) / 32);
+    const int max_by_len = std::max(1, seqlen_k_capacity / 512);
+    const int64_t want = (2 * int64_t(std::max(num_cus, 1)) + wgs - 1) / std::max<int64_t>(wgs, 1);
+    return int(std::max<int64_t>(1, std::min<int64_t>({want, int64_t(max_by_len), 128})));
+}
+
+extern "C" size_t fa_kv_workspace_bytes(const fa_kvcache_args *a) {
+    if (!a || a->num_splits <= 1) return 0;
+    const size_t rows = size_t(a->batch) * a->nheads * a->seqlen_q;
+    return size_t(a->num_splits) * rows * (size_t(a->head_dim) + 1) * sizeof(float);
+}
+
+extern "C" int fa_kv_append(const fa_kvcache_args *args, void *stream) {
+    int rc = fa::check_kv(args);
+    if (rc) return rc;
+    const fa_kvcache_args &a = *args;
+    if (!a.k_new.ptr || a.seqlen_new == 0 || a.batch == 0) return FA_OK;
+    if (!a.v_new.ptr || fa_check_tensor(a.k_new, true) || fa_check_tensor(a.v_new, true) ||
+        fa_check_tensor(a.k_cache, true) || fa_check_tensor(a.v_cache, true))
+        return FA_ERR_INVALID_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t total = int64_t(a.batch) * a.seqlen_new * a.nheads_k * (a.head_dim / 8);
+    const int64_t blocks = (total + 255) / 256;
+    if (a.head_dim == 128)
+        hipLaunchKernelGGL(fa::kv_append_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(fa::kv_append_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    return int(hipGetLastError());
+}
+
+extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
+    int rc = fa::check_kv(args);
+    if (rc) return rc;
+    const fa_kvcache_args &a = *args;
+    if (fa_check_tensor(a.q, true) || fa_check_tensor(a.o, true) || fa_check_tensor(a.k_cache, true) ||
+        fa_check_tensor(a.v_cache, true))
+        return FA_ERR_INVALID_ARG;
+    if (a.num_splits > 1 && (!a.out_accum || !a.lse_accum)) return FA_ERR_WORKSPACE;
+    const int R = (a.nheads / a.nheads_k) * a.seqlen_q;
+    const int row_tiles = (R + 31) / 32;
+    const int64_t gx = int64_t(a.batch) * a.nheads_k * row_tiles;
+    if (gx == 0) return FA_OK;
+    if (gx > 0x7fffffff || a.num_splits > 65535) return FA_ERR_INVALID_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(unsigned(gx), unsigned(a.num_splits));
+    if (a.head_dim == 128)
+        hipLaunchKernelGGL(fa::kv_splitkv_kernel<128>, grid, dim3(fa::kKvThreads), 0, s, a, row_tiles);
+    else
+        hipLaunchKernelGGL(fa::kv_splitkv_kernel<64>, grid, dim3(fa::kKvThreads), 0, s, a, row_tiles);
+    return int(hipGetLastError());
+}
+
+extern "C" int fa_kv_combine(const fa_kvcache_args *args, void *stream) {
+    int rc = fa::check_kv(args);
+    if (rc) return rc;
+    const fa_kvcache_args &a = *args;
+    if (a.num_splits <= 1) return FA_OK;
+    if (!a.out_accum || !a.lse_accum) return FA_ERR_WORKSPACE;
+    const int64_t nrow = int64_t(a.batch) * a.nheads * a.seqlen_q;
+    if (nrow == 0) return FA_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t blocks = (nrow + 3) / 4;
+    if (a.head_dim == 128)
+        hipLaunchKernelGGL(fa::kv_combine_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(fa::kv_combine_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    return int(hipGetLastError());
+}
+
+extern "C" int fa_fwd_kvcache(const fa_kvcache_args *args, void *stream) {
+    int rc = fa_kv_append(args, stream);
+    if (rc) return rc;
+    rc = fa_kv_splitkv(args, stream);
+    if (rc) return rc;
+    return fa_kv_combine(args, stream);
+}

@@ -1,0 +1,484 @@
+// Host layer: the `flash_attn_turing` Python extension over the C ABI of
+// libfa_mi355x.so (include/fa_mi355x.h).
+//
+// Mirrors the reference's pybind module (csrc/flash_attn/flash_api.cpp:717-724):
+// the same five bindings (fwd, bwd, varlen_fwd, varlen_bwd, fwd_kvcache), the
+// same argument order, the same TORCH_CHECK conditions and messages, and the
+// same [b, h, seqlen_q] / [b, h, max_seqlen_q] LSE layout.  Differences, all
+// deliberate:
+//   * every kernel runs on the current HIP stream under a device guard (the
+//     reference launched fwd/bwd on the legacy default stream);
+//   * outputs are allocated with `empty` where the kernels write every element
+//     (the reference zero-filled them because early-exit CTAs wrote nothing);
+//   * the GQA dK/dV sum is done inside the dK/dV kernel (no expanded
+//     per-q-head buffers, no torch::sum_out);
+//   * the KV append is one device kernel for contiguous, remapped and paged
+//     caches (no host loop over the batch), and the chunked KV path reads the
+//     cache through cache_batch_idx in-kernel (no index_select copy);
+//   * inputs must be float16 on the GPU; tensors whose strides or base address
+//     are not 16-byte aligned are made contiguous before the launch.
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
+
+#include <optional>
+#include <vector>
+
+#include "fa_mi355x.h"
+
+namespace {
+
+inline void check_supported_head_dim(const int64_t head_size) {
+    TORCH_CHECK(head_size == 64 || head_size == 128, "Turing FlashAttention supports head_dim 64 or 128");
+}
+
+inline void check_fp16_cuda(const at::Tensor &t, const char *name) {
+    TORCH_CHECK(t.is_cuda(), name, " must be a CUDA (HIP) tensor");
+    TORCH_CHECK(t.scalar_type() == at::kHalf, name, " must be a float16 tensor");
+}
+
+// 16-byte aligned base and strides (in elements, multiple of 8), last dim contiguous.
+inline at::Tensor aligned(const at::Tensor &t) {
+    bool ok = t.stride(-1) == 1 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
+    for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = (t.stride(i) % 8) == 0 || t.size(i) == 1;
+    return ok ? t : t.contiguous();
+}
+
+inline fa_tensor desc4(const at::Tensor &t) {  // [batch][row][head][d]
+    return fa_tensor{t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)};
+}
+inline fa_tensor desc3(const at::Tensor &t) {  // packed [total][head][d]
+    return fa_tensor{t.data_ptr(), 0, t.stride(0), t.stride(1)};
+}
+
+inline hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); }
+
+inline void check_rc(int rc, const char *what) {
+    TORCH_CHECK(rc == FA_OK, what, " failed: ", fa_error_string(rc));
+}
+
+int num_cus(int device) {
+    static int cached[64] = {0};
+    if (device >= 0 && device < 64 && cached[device]) return cached[device];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
+    if (device >= 0 && device < 64) cached[device] = n;
+    return n;
+}
+
+}  // namespace
+
+std::vector<at::Tensor> mha_fwd(at::Tensor q, at::Tensor k, at::Tensor v, const float softmax_scale, bool is_causal) {
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "q, k, v must be rank-4 tensors");
+    const int64_t batch_size = q.size(0), seqlen_q = q.size(1), num_heads = q.size(2), head_size = q.size(3);
+    const int64_t seqlen_k = k.size(1), num_heads_k = k.size(2);
+    TORCH_CHECK(k.size(0) == batch_size && v.size(0) == batch_size, "k/v batch size must match q");
+    TORCH_CHECK(v.size(1) == seqlen_k, "k and v seqlen_k must match");
+    TORCH_CHECK(v.size(2) == num_heads_k, "k and v num_heads must match");
+    TORCH_CHECK(k.size(3) == head_size && v.size(3) == head_size, "q/k/v head_dim must match");
+    TORCH_CHECK(num_heads % num_heads_k == 0, "num_heads_q must be divisible by num_heads_k for GQA/MQA");
+    check_supported_head_dim(head_size);
+    check_fp16_cuda(q, "q");
+    check_fp16_cuda(k, "k");
+    check_fp16_cuda(v, "v");
+    c10::DeviceGuard guard(q.device());
+    q = aligned(q);
+    k = aligned(k);
+    v = aligned(v);
+
+    at::Tensor o = at::empty(q.sizes(), q.options());
+    at::Tensor l = at::empty({batch_size, num_heads, seqlen_q}, q.options().dtype(at::kFloat));
+
+    fa_fwd_args a{};
+    a.q = desc4(q);
+    a.k = desc4(k);
+    a.v = desc4(v);
+    a.o = desc4(o);
+    a.lse = l.data_ptr<float>();
+    a.batch = int32_t(batch_size);
+    a.seqlen_q = int32_t(seqlen_q);
+    a.seqlen_k = int32_t(seqlen_k);
+    a.nheads = int32_t(num_heads);
+    a.nheads_k = int32_t(num_heads_k);
+    a.head_dim = int32_t(head_size);
+    a.lse_seqlen = int32_t(seqlen_q);
+    a.softmax_scale = softmax_scale;
+    a.causal = is_causal ? 1 : 0;
+    check_rc(fa_fwd(&a, current_stream()), "fa_fwd");
+    return {o, l};
+}
+
+std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor out, at::Tensor l,
+                                at::Tensor dout, const float softmax_scale, bool is_causal) {
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "q, k, v must be rank-4 tensors");
+    TORCH_CHECK(out.dim() == 4 && dout.dim() == 4, "out and dout must be rank-4 tensors");
+    const int64_t batch_size = q.size(0), seqlen_q = q.size(1), num_heads = q.size(2), head_size = q.size(3);
+    const int64_t seqlen_k = k.size(1), num_heads_k = k.size(2);
+    TORCH_CHECK(k.size(0) == batch_size && v.size(0) == batch_size, "k/v batch size must match q");
+    TORCH_CHECK(v.size(1) == seqlen_k, "k and v seqlen_k must match");
+    TORCH_CHECK(v.size(2) == num_heads_k, "k and v num_heads must match");
+    TORCH_CHECK(k.size(3) == head_size && v.size(3) == head_size, "q/k/v head_dim must match");
+    TORCH_CHECK(out.sizes() == q.sizes() && dout.sizes() == q.sizes(), "out and dout must match q shape");
+    TORCH_CHECK(num_heads % num_heads_k == 0, "num_heads_q must be divisible by num_heads_k for GQA/MQA");
+    check_supported_head_dim(head_size);
+    for (auto *t : {&q, &k, &v, &out, &dout}) check_fp16_cuda(*t, "q, k, v, out and dout");
+    TORCH_CHECK(l.is_cuda() && l.scalar_type() == at::kFloat && l.dim() == 3 && l.size(0) == batch_size &&
+                    l.size(1) == num_heads && l.size(2) == seqlen_q && l.is_contiguous(),
+                "l must be a contiguous float32 tensor of shape [batch_size, nheads_q, seqlen_q]");
+    c10::DeviceGuard guard(q.device());
+    q = aligned(q);
+    k = aligned(k);
+    v = aligned(v);
+    out = aligned(out);
+    dout = aligned(dout);
+
+    at::Tensor dq = at::empty(q.sizes(), q.options());
+    at::Tensor dk = at::empty(k.sizes(), k.options());
+    at::Tensor dv = at::empty(v.sizes(), v.options());
+    at::Tensor dsum = at::empty(l.sizes(), l.options());
+
+    fa_bwd_args a{};
+    a.q = desc4(q);
+    a.k = desc4(k);
+    a.v = desc4(v);
+    a.o = desc4(out);
+    a.dout = desc4(dout);
+    a.dq = desc4(dq);
+    a.dk = desc4(dk);
+    a.dv = desc4(dv);
+    a.lse = l.data_ptr<float>();
+    a.dsum = dsum.data_ptr<float>();
+    a.batch = int32_t(batch_size);
+    a.seqlen_q = int32_t(seqlen_q);
+    a.seqlen_k = int32_t(seqlen_k);
+    a.nheads = int32_t(num_heads);
+    a.nheads_k = int32_t(num_heads_k);
+    a.head_dim = int32_t(head_size);
+    a.lse_seqlen = int32_t(seqlen_q);
+    a.softmax_scale = softmax_scale;
+    a.causal = is_causal ? 1 : 0;
+    check_rc(fa_bwd(&a, current_stream()), "fa_bwd");
+    return {dq, dk, dv};
+}
+
+static void check_cu_seqlens(const at::Tensor &cu_seqlens_q, const at::Tensor &cu_seqlens_k) {
+    TORCH_CHECK(cu_seqlens_q.is_cuda() && cu_seqlens_k.is_cuda(), "cu_seqlens_q/cu_seqlens_k must be CUDA tensors");
+    TORCH_CHECK(cu_seqlens_q.scalar_type() == at::kInt && cu_seqlens_k.scalar_type() == at::kInt,
+                "cu_seqlens_q/cu_seqlens_k must be int32 tensors");
+    TORCH_CHECK(cu_seqlens_q.is_contiguous() && cu_seqlens_k.is_contiguous(),
+                "cu_seqlens_q/cu_seqlens_k must be contiguous");
+    TORCH_CHECK(cu_seqlens_q.dim() == 1 && cu_seqlens_k.dim() == 1, "cu_seqlens_q/cu_seqlens_k must be rank-1");
+    TORCH_CHECK(cu_seqlens_q.numel() >= 2 && cu_seqlens_k.numel() >= 2,
+                "cu_seqlens_q/cu_seqlens_k must have at least 2 elements");
+    TORCH_CHECK(cu_seqlens_k.numel() == cu_seqlens_q.numel(),
+                "cu_seqlens_k must have shape [batch_size + 1] with cumulative offsets");
+}
+
+static void check_varlen_qkv(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v) {
+    TORCH_CHECK(k.size(0) == v.size(0), "k and v total tokens must match");
+    TORCH_CHECK(k.size(1) == v.size(1), "k and v num_heads must match");
+    TORCH_CHECK(k.size(2) == v.size(2), "k and v head_dim must match");
+    TORCH_CHECK(q.size(2) == k.size(2), "q/k/v head_dim must match");
+    TORCH_CHECK(q.size(1) % k.size(1) == 0, "num_heads_q must be divisible by num_heads_k for GQA/MQA");
+}
+
+std::vector<at::Tensor> mha_varlen_fwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor &cu_seqlens_q,
+                                       at::Tensor &cu_seqlens_k, const int max_seqlen_q, const int max_seqlen_k,
+                                       const float softmax_scale, bool is_causal) {
+    TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "q, k, v must be rank-3 packed tensors");
+    check_cu_seqlens(cu_seqlens_q, cu_seqlens_k);
+    const int64_t batch_size = cu_seqlens_q.numel() - 1;
+    check_varlen_qkv(q, k, v);
+    const int64_t num_heads = q.size(1), num_heads_k = k.size(1), head_size = q.size(2);
+    check_supported_head_dim(head_size);
+    TORCH_CHECK(max_seqlen_q >= 0 && max_seqlen_k >= 0, "max_seqlen_q/max_seqlen_k must be non-negative");
+    check_fp16_cuda(q, "q");
+    check_fp16_cuda(k, "k");
+    check_fp16_cuda(v, "v");
+    c10::DeviceGuard guard(q.device());
+    q = aligned(q);
+    k = aligned(k);
+    v = aligned(v);
+
+    // Packed rows past cu_seqlens_q[-1] belong to no sequence and stay 0.
+    at::Tensor out = at::zeros(q.sizes(), q.options());
+    at::Tensor l = at::empty({batch_size, num_heads, max_seqlen_q}, q.options().dtype(at::kFloat));
+
+    fa_fwd_args a{};
+    a.q = desc3(q);
+    a.k = desc3(k);
+    a.v = desc3(v);
+    a.o = desc3(out);
+    a.lse = l.data_ptr<float>();
+    a.cu_seqlens_q = cu_seqlens_q.data_ptr<int32_t>();
+    a.cu_seqlens_k = cu_seqlens_k.data_ptr<int32_t>();
+    a.batch = int32_t(batch_size);
+    a.seqlen_q = max_seqlen_q;
+    a.seqlen_k = max_seqlen_k;
+    a.nheads = int32_t(num_heads);
+    a.nheads_k = int32_t(num_heads_k);
+    a.head_dim = int32_t(head_size);
+    a.lse_seqlen = max_seqlen_q;
+    a.softmax_scale = softmax_scale;
+    a.causal = is_causal ? 1 : 0;
+    check_rc(fa_fwd(&a, current_stream()), "fa_fwd (varlen)");
+    return {out, l};
+}
+
+std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor out, at::Tensor l,
+                                       at::Tensor dout, at::Tensor cu_seqlens_q, at::Tensor cu_seqlens_k,
+                                       const int max_seqlen_q, const int max_seqlen_k, const float softmax_scale,
+                                       bool is_causal) {
+    TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "q, k, v must be rank-3 packed tensors");
+    check_cu_seqlens(cu_seqlens_q, cu_seqlens_k);
+    const int64_t batch_size = cu_seqlens_q.numel() - 1;
+    check_varlen_qkv(q, k, v);
+    TORCH_CHECK(out.sizes() == q.sizes(), "out must match q shape");
+    TORCH_CHECK(dout.sizes() == q.sizes(), "dout must match q shape");
+    TORCH_CHECK(l.dim() == 3, "l must be rank-3 for varlen_bwd");
+    const int64_t num_heads = q.size(1), num_heads_k = k.size(1), head_size = q.size(2);
+    check_supported_head_dim(head_size);
+    TORCH_CHECK(l.size(0) == batch_size && l.size(1) == num_heads && l.size(2) == max_seqlen_q,
+                "l must have shape [batch_size, nheads_q, max_seqlen_q]");
+    for (auto *t : {&q, &k, &v, &out, &dout}) check_fp16_cuda(*t, "q, k, v, out and dout");
+    TORCH_CHECK(l.is_cuda() && l.scalar_type() == at::kFloat && l.is_contiguous(),
+                "l must be a contiguous float32 CUDA tensor");
+    c10::DeviceGuard guard(q.device());
+    q = aligned(q);
+    k = aligned(k);
+    v = aligned(v);
+    out = aligned(out);
+    dout = aligned(dout);
+
+    // Packed rows past the last sequence belong to no sequence and stay 0.
+    at::Tensor dq = at::zeros(q.sizes(), q.options());
+    at::Tensor dk = at::zeros(k.sizes(), k.options());
+    at::Tensor dv = at::zeros(v.sizes(), v.options());
+    at::Tensor dsum = at::empty(l.sizes(), l.options());
+
+    fa_bwd_args a{};
+    a.q = desc3(q);
+    a.k = desc3(k);
+    a.v = desc3(v);
+    a.o = desc3(out);
+    a.dout = desc3(dout);
+    a.dq = desc3(dq);
+    a.dk = desc3(dk);
+    a.dv = desc3(dv);
+    a.lse = l.data_ptr<float>();
+    a.dsum = dsum.data_ptr<float>();
+    a.cu_seqlens_q = cu_seqlens_q.data_ptr<int32_t>();
+    a.cu_seqlens_k = cu_seqlens_k.data_ptr<int32_t>();
+    a.batch = int32_t(batch_size);
+    a.seqlen_q = max_seqlen_q;
+    a.seqlen_k = max_seqlen_k;
+    a.nheads = int32_t(num_heads);
+    a.nheads_k = int32_t(num_heads_k);
+    a.head_dim = int32_t(head_size);
+    a.lse_seqlen = max_seqlen_q;
+    a.softmax_scale = softmax_scale;
+    a.causal = is_causal ? 1 : 0;
+    check_rc(fa_bwd(&a, current_stream()), "fa_bwd (varlen)");
+    return {dq, dk, dv};
+}
+
+std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
+                                        std::optional<at::Tensor> k_opt, std::optional<at::Tensor> v_opt,
+                                        at::Tensor cache_seqlens, std::optional<at::Tensor> rotary_cos,
+                                        std::optional<at::Tensor> rotary_sin,
+                                        std::optional<at::Tensor> cache_batch_idx_opt,
+                                        std::optional<at::Tensor> cache_leftpad,
+                                        std::optional<at::Tensor> block_table_opt,
+                                        std::optional<at::Tensor> alibi_slopes, std::optional<at::Tensor> out_opt,
+                                        const float softmax_scale, bool is_causal, int window_size_left,
+                                        int window_size_right, const float softcap, bool rotary_interleaved,
+                                        int num_splits) {
+    // Order and texts follow flash_api.cpp:530-628.
+    (void)rotary_interleaved;
+    TORCH_CHECK(!rotary_cos.has_value() && !rotary_sin.has_value(),
+                "Turing KV-cache does not support rotary embeddings yet");
+    TORCH_CHECK(!cache_leftpad.has_value(), "Turing KV-cache does not support cache_leftpad yet");
+    TORCH_CHECK(!alibi_slopes.has_value(), "Turing KV-cache does not support ALiBi yet");
+    TORCH_CHECK(!out_opt.has_value(), "Turing KV-cache does not support a preallocated output tensor yet");
+    TORCH_CHECK(window_size_left == -1 && window_size_right == -1,
+                "Turing KV-cache does not support local window attention yet");
+    TORCH_CHECK(softcap == 0.0f, "Turing KV-cache does not support softcap yet");
+    TORCH_CHECK(num_splits >= 0, "num_splits must be non-negative");
+
+    TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda(), "q, k_cache, v_cache must be CUDA tensors");
+    TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                    v_cache.scalar_type() == at::kHalf,
+                "q, k_cache, v_cache must be float16 tensors");
+    TORCH_CHECK(q.dim() == 4 && k_cache.dim() == 4 && v_cache.dim() == 4, "q, k_cache, v_cache must be rank-4 tensors");
+    TORCH_CHECK(k_cache.size(1) == v_cache.size(1), "k_cache and v_cache seqlen must match");
+    TORCH_CHECK(k_cache.size(2) == v_cache.size(2), "k_cache and v_cache num_heads must match");
+    TORCH_CHECK(q.size(3) == k_cache.size(3) && q.size(3) == v_cache.size(3), "q, k_cache, v_cache head_dim must match");
+    TORCH_CHECK(q.size(2) % k_cache.size(2) == 0, "num_heads_q must be divisible by num_heads_k for GQA/MQA");
+    check_supported_head_dim(q.size(3));
+    TORCH_CHECK(q.stride(-1) == 1 && k_cache.stride(-1) == 1 && v_cache.stride(-1) == 1,
+                "q, k_cache, v_cache must have contiguous last dimension");
+    TORCH_CHECK(cache_seqlens.is_cuda(), "cache_seqlens must be a CUDA tensor");
+    TORCH_CHECK(cache_seqlens.scalar_type() == at::kInt, "cache_seqlens must be an int32 tensor");
+    TORCH_CHECK(cache_seqlens.is_contiguous(), "cache_seqlens must be contiguous");
+    TORCH_CHECK(cache_seqlens.dim() == 1 && cache_seqlens.numel() == q.size(0),
+                "cache_seqlens must have shape [batch_size]");
+
+    const int64_t batch_size = q.size(0), seqlen_q = q.size(1), num_heads = q.size(2), head_size = q.size(3);
+    const int64_t num_heads_k = k_cache.size(2);
+    const bool has_block_table = block_table_opt.has_value();
+    at::Tensor block_table;
+    int64_t page_block_size = 0;
+    int64_t seqlen_cache = k_cache.size(1);
+    int64_t batch_size_cache = k_cache.size(0);
+    if (has_block_table) {
+        block_table = *block_table_opt;
+        TORCH_CHECK(block_table.is_cuda(), "block_table must be a CUDA tensor");
+        TORCH_CHECK(block_table.scalar_type() == at::kInt, "block_table must be an int32 tensor");
+        TORCH_CHECK(block_table.stride(-1) == 1, "block_table must have contiguous last dimension");
+        TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == batch_size,
+                    "block_table must have shape [batch_size, max_num_blocks_per_seq]");
+        page_block_size = k_cache.size(1);
+        TORCH_CHECK(page_block_size % 256 == 0, "Paged KV cache block size must be divisible by 256");
+        seqlen_cache = block_table.size(1) * page_block_size;
+        batch_size_cache = batch_size;
+    }
+
+    at::Tensor cache_batch_idx;
+    const bool has_cache_batch_idx = cache_batch_idx_opt.has_value();
+    if (has_cache_batch_idx) {
+        TORCH_CHECK(!has_block_table, "Paged KV cache does not support cache_batch_idx");
+        cache_batch_idx = *cache_batch_idx_opt;
+        TORCH_CHECK(cache_batch_idx.is_cuda(), "cache_batch_idx must be a CUDA tensor");
+        TORCH_CHECK(cache_batch_idx.scalar_type() == at::kInt, "cache_batch_idx must be an int32 tensor");
+        TORCH_CHECK(cache_batch_idx.is_contiguous(), "cache_batch_idx must be contiguous");
+        TORCH_CHECK(cache_batch_idx.dim() == 1 && cache_batch_idx.numel() == batch_size,
+                    "cache_batch_idx must have shape [batch_size]");
+    } else {
+        TORCH_CHECK(batch_size == batch_size_cache,
+                    "q and cache batch size must match when cache_batch_idx is not provided");
+    }
+
+    at::Tensor k, v;
+    const bool has_k = k_opt.has_value(), has_v = v_opt.has_value();
+    TORCH_CHECK(has_k == has_v, "k and v must either both be provided or both be None");
+    int64_t seqlen_new = 0;
+    if (has_k) {
+        k = *k_opt;
+        v = *v_opt;
+        TORCH_CHECK(k.is_cuda() && v.is_cuda(), "k and v must be CUDA tensors");
+        TORCH_CHECK(k.scalar_type() == at::kHalf && v.scalar_type() == at::kHalf, "k and v must be float16 tensors");
+        TORCH_CHECK(k.dim() == 4 && v.dim() == 4, "k and v must be rank-4 tensors");
+        TORCH_CHECK(k.size(0) == batch_size && v.size(0) == batch_size, "k/v batch size must match q");
+        TORCH_CHECK(k.size(1) == v.size(1), "k and v seqlen must match");
+        TORCH_CHECK(k.size(2) == num_heads_k && v.size(2) == num_heads_k, "k/v num_heads must match the cache num_heads");
+        TORCH_CHECK(k.size(3) == head_size && v.size(3) == head_size, "k/v head_dim must match q");
+        TORCH_CHECK(k.stride(-1) == 1 && v.stride(-1) == 1, "k and v must have contiguous last dimension");
+        seqlen_new = k.size(1);
+    }
+
+    c10::DeviceGuard guard(q.device());
+    // Host-visible checks keep the reference's semantics (two device-to-host reads).
+    if (batch_size > 0) {
+        const int64_t max_end = cache_seqlens.max().item<int>() + seqlen_new;
+        TORCH_CHECK(max_end <= seqlen_cache, "cache capacity is insufficient for the requested append length");
+    }
+    if (has_cache_batch_idx && batch_size > 0) {
+        at::Tensor idx_cpu = cache_batch_idx.to(at::kCPU);
+        const int32_t *p = idx_cpu.data_ptr<int32_t>();
+        for (int64_t i = 0; i < batch_size; ++i)
+            TORCH_CHECK(p[i] >= 0 && p[i] < batch_size_cache, "cache_batch_idx entries must be within cache batch bounds");
+    }
+
+    q = aligned(q);
+    TORCH_CHECK(((reinterpret_cast<uintptr_t>(k_cache.data_ptr()) | reinterpret_cast<uintptr_t>(v_cache.data_ptr())) &
+                 15u) == 0 &&
+                    k_cache.stride(0) % 8 == 0 && k_cache.stride(1) % 8 == 0 && k_cache.stride(2) % 8 == 0 &&
+                    v_cache.stride(0) % 8 == 0 && v_cache.stride(1) % 8 == 0 && v_cache.stride(2) % 8 == 0,
+                "k_cache and v_cache must be 16-byte aligned with strides that are multiples of 8 elements");
+    if (has_k) {
+        k = aligned(k);
+        v = aligned(v);
+    }
+
+    at::Tensor out = at::empty(q.sizes(), q.options());
+    at::Tensor lse = at::empty({batch_size, num_heads, seqlen_q}, q.options().dtype(at::kFloat));
+    hipStream_t stream = current_stream();
+
+    fa_kvcache_args a{};
+    a.q = desc4(q);
+    a.k_cache = desc4(k_cache);
+    a.v_cache = desc4(v_cache);
+    if (has_k) {
+        a.k_new = desc4(k);
+        a.v_new = desc4(v);
+    }
+    a.o = desc4(out);
+    a.lse = lse.data_ptr<float>();
+    a.cache_seqlens = cache_seqlens.data_ptr<int32_t>();
+    a.cache_batch_idx = has_cache_batch_idx ? cache_batch_idx.data_ptr<int32_t>() : nullptr;
+    a.block_table = has_block_table ? block_table.data_ptr<int32_t>() : nullptr;
+    a.block_table_stride = has_block_table ? block_table.stride(0) : 0;
+    a.batch = int32_t(batch_size);
+    a.seqlen_q = int32_t(seqlen_q);
+    a.nheads = int32_t(num_heads);
+    a.nheads_k = int32_t(num_heads_k);
+    a.head_dim = int32_t(head_size);
+    a.seqlen_new = int32_t(seqlen_new);
+    a.page_block_size = int32_t(page_block_size);
+    a.softmax_scale = softmax_scale;
+    a.causal = is_causal ? 1 : 0;
+    a.num_splits = 1;
+
+    check_rc(fa_kv_append(&a, stream), "fa_kv_append");
+
+    // Routing of flash_api.cpp:668: paged, explicit splits > 1 or single-token decode
+    // take the split-KV kernel; a contiguous multi-token chunk takes the tiled
+    // forward kernel with per-batch key counts and the batch remap.
+    const bool use_split_kernel = has_block_table || num_splits > 1 || seqlen_q == 1;
+    if (use_split_kernel) {
+        a.num_splits = fa_kv_num_splits(num_splits, int(seqlen_cache), int(head_size), int(seqlen_q),
+                                        int(batch_size), int(num_heads), int(num_heads_k),
+                                        num_cus(q.get_device()));
+        at::Tensor ws;
+        if (a.num_splits > 1) {
+            const int64_t rows = batch_size * num_heads * seqlen_q;
+            ws = at::empty({a.num_splits * rows * (head_size + 1)}, q.options().dtype(at::kFloat));
+            a.out_accum = ws.data_ptr<float>();
+            a.lse_accum = a.out_accum + a.num_splits * rows * head_size;
+        }
+        check_rc(fa_kv_splitkv(&a, stream), "fa_kv_splitkv");
+        check_rc(fa_kv_combine(&a, stream), "fa_kv_combine");
+        return {out, lse};
+    }
+
+    fa_fwd_args f{};
+    f.q = desc4(q);
+    f.k = desc4(k_cache);
+    f.v = desc4(v_cache);
+    f.o = desc4(out);
+    f.lse = lse.data_ptr<float>();
+    f.seqused_k = cache_seqlens.data_ptr<int32_t>();
+    f.seqused_k_add = int32_t(seqlen_new);
+    f.k_batch_idx = a.cache_batch_idx;
+    f.batch = int32_t(batch_size);
+    f.seqlen_q = int32_t(seqlen_q);
+    f.seqlen_k = int32_t(seqlen_cache);
+    f.nheads = int32_t(num_heads);
+    f.nheads_k = int32_t(num_heads_k);
+    f.head_dim = int32_t(head_size);
+    f.lse_seqlen = int32_t(seqlen_q);
+    f.softmax_scale = softmax_scale;
+    f.causal = is_causal ? 1 : 0;
+    check_rc(fa_fwd(&f, stream), "fa_fwd (kv-cache chunk)");
+    return {out, lse};
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("fwd", &mha_fwd, "Forward pass");
+    m.def("bwd", &mha_bwd, "Backward pass");
+    m.def("varlen_fwd", &mha_varlen_fwd, "Varlen forward pass");
+    m.def("varlen_bwd", &mha_varlen_bwd, "Varlen backward pass");
+    m.def("fwd_kvcache", &mha_fwd_kvcache, "KV-cache forward pass");
+}

@@ -1,0 +1,416 @@
+"""Python interface of the MI355X FlashAttention (drop-in for the reference's
+flash_attention_interface.py).
+
+Public API, argument order, defaults, validation order and error messages follow
+the reference module (flash_attention_interface.py:448-922):
+
+    flash_attn_func, flash_attn_qkvpacked_func, flash_attn_kvpacked_func,
+    flash_attn_varlen_func, flash_attn_varlen_qkvpacked_func,
+    flash_attn_varlen_kvpacked_func, flash_attn_with_kvcache
+
+and the autograd classes FlashAttnFunc, FlashAttnQKVPackedFunc,
+FlashAttnKVPackedFunc, FlashAttnVarlenFunc, FlashAttnVarlenQKVPackedFunc,
+FlashAttnVarlenKVPackedFunc (:172-445).  Every call goes to the native
+``flash_attn_turing`` extension (HIP kernels for gfx950); there is no Python
+math fallback: a missing or incompatible extension raises at import or call.
+"""
+
+from typing import Optional, Tuple, Union
+
+import torch  # noqa: F401  (loads the HIP runtime before the extension)
+
+import flash_attn_turing as flash_attn_gpu
+
+
+def maybe_contiguous(x: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """Copy only tensors whose last dimension is strided (interface.py:9-10)."""
+    if x is None or x.stride(-1) == 1:
+        return x
+    return x.contiguous()
+
+
+def _default_scale(q: torch.Tensor, softmax_scale: Optional[float]) -> float:
+    # interface.py:183: head_dim ** -0.5 unless given.
+    return q.shape[-1] ** (-0.5) if softmax_scale is None else softmax_scale
+
+
+# ---------------------------------------------------------------------------
+# Thin wrappers over the extension (interface.py:13-169).
+
+
+def _flash_attn_forward(q, k, v, softmax_scale: float, causal: bool):
+    q, k, v = (maybe_contiguous(t) for t in (q, k, v))
+    out, lse = flash_attn_gpu.fwd(q, k, v, softmax_scale, causal)
+    return out, lse
+
+
+def _flash_attn_backward(dout, q, k, v, out, lse, softmax_scale: float, causal: bool):
+    dout, q, k, v, out, lse = (maybe_contiguous(t) for t in (dout, q, k, v, out, lse))
+    dq, dk, dv = flash_attn_gpu.bwd(q, k, v, out, lse, dout, softmax_scale, causal)
+    return dq, dk, dv
+
+
+def _flash_attn_varlen_forward(
+    q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float, causal: bool
+):
+    q, k, v = (maybe_contiguous(t) for t in (q, k, v))
+    out, lse = flash_attn_gpu.varlen_fwd(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal
+    )
+    return out, lse
+
+
+def _flash_attn_varlen_backward(
+    dout,
+    q,
+    k,
+    v,
+    out,
+    lse,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    causal: bool,
+):
+    dout, q, k, v, out, lse = (maybe_contiguous(t) for t in (dout, q, k, v, out, lse))
+    dq, dk, dv = flash_attn_gpu.varlen_bwd(
+        q, k, v, out, lse, dout, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal
+    )
+    return dq, dk, dv
+
+
+def _flash_attn_kvcache_forward(
+    q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale: float, causal: bool,
+    num_splits: int,
+):
+    tensors = (q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table)
+    q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table = (maybe_contiguous(t) for t in tensors)
+    # The 20-argument binding of flash_api.cpp:508-528; rotary, leftpad, ALiBi,
+    # a preallocated out, local windows and softcap are passed as "absent".
+    out, lse = flash_attn_gpu.fwd_kvcache(
+        q, k_cache, v_cache, k, v, cache_seqlens,
+        None, None,            # rotary_cos, rotary_sin
+        cache_batch_idx,
+        None,                  # cache_leftpad
+        block_table,
+        None, None,            # alibi_slopes, out
+        softmax_scale, causal,
+        -1, -1,                # window_size_left, window_size_right
+        0.0,                   # softcap
+        True,                  # rotary_interleaved
+        num_splits,
+    )
+    return out, lse
+
+
+# ---------------------------------------------------------------------------
+# Autograd functions (interface.py:172-445).
+
+
+class FlashAttnFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, softmax_scale, causal, is_grad_enabled):
+        softmax_scale = _default_scale(q, softmax_scale)
+        out, lse = _flash_attn_forward(q, k, v, softmax_scale, causal)
+        if is_grad_enabled and (q.requires_grad or k.requires_grad or v.requires_grad):
+            ctx.save_for_backward(q, k, v, out, lse)
+            ctx.softmax_scale, ctx.causal = softmax_scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal)
+        return dq, dk, dv, None, None, None
+
+
+def _unpack(packed: torch.Tensor, dim: int, n: int):
+    return tuple(packed.select(dim=dim, index=i).contiguous() for i in range(n))
+
+
+def _repack(parts, dim: int) -> torch.Tensor:
+    return torch.stack(parts, dim=dim)
+
+
+class FlashAttnQKVPackedFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, qkv, softmax_scale, causal, is_grad_enabled):
+        q, k, v = _unpack(qkv, 2, 3)
+        softmax_scale = _default_scale(q, softmax_scale)
+        out, lse = _flash_attn_forward(q, k, v, softmax_scale, causal)
+        if is_grad_enabled and qkv.requires_grad:
+            ctx.save_for_backward(q, k, v, out, lse)
+            ctx.softmax_scale, ctx.causal = softmax_scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal)
+        return _repack((dq, dk, dv), 2), None, None, None
+
+
+class FlashAttnKVPackedFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, kv, softmax_scale, causal, is_grad_enabled):
+        k, v = _unpack(kv, 2, 2)
+        softmax_scale = _default_scale(q, softmax_scale)
+        out, lse = _flash_attn_forward(q, k, v, softmax_scale, causal)
+        if is_grad_enabled and (q.requires_grad or kv.requires_grad):
+            ctx.save_for_backward(q, k, v, out, lse)
+            ctx.softmax_scale, ctx.causal = softmax_scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal)
+        return dq, _repack((dk, dv), 2), None, None, None
+
+
+class FlashAttnVarlenFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
+                is_grad_enabled):
+        softmax_scale = _default_scale(q, softmax_scale)
+        out, lse = _flash_attn_varlen_forward(
+            q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal
+        )
+        if is_grad_enabled and (q.requires_grad or k.requires_grad or v.requires_grad):
+            ctx.save_for_backward(q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k)
+            ctx.max_seqlen_q, ctx.max_seqlen_k = max_seqlen_q, max_seqlen_k
+            ctx.softmax_scale, ctx.causal = softmax_scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_varlen_backward(
+            dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
+            ctx.softmax_scale, ctx.causal,
+        )
+        return dq, dk, dv, None, None, None, None, None, None, None
+
+
+class FlashAttnVarlenQKVPackedFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, qkv, cu_seqlens, max_seqlen, softmax_scale, causal, is_grad_enabled):
+        q, k, v = _unpack(qkv, 1, 3)
+        softmax_scale = _default_scale(q, softmax_scale)
+        out, lse = _flash_attn_varlen_forward(
+            q, k, v, cu_seqlens, cu_seqlens, max_seqlen, max_seqlen, softmax_scale, causal
+        )
+        if is_grad_enabled and qkv.requires_grad:
+            ctx.save_for_backward(q, k, v, out, lse, cu_seqlens)
+            ctx.max_seqlen = max_seqlen
+            ctx.softmax_scale, ctx.causal = softmax_scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, cu_seqlens = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_varlen_backward(
+            dout, q, k, v, out, lse, cu_seqlens, cu_seqlens, ctx.max_seqlen, ctx.max_seqlen,
+            ctx.softmax_scale, ctx.causal,
+        )
+        return _repack((dq, dk, dv), 1), None, None, None, None, None
+
+
+class FlashAttnVarlenKVPackedFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
+                is_grad_enabled):
+        k, v = _unpack(kv, 1, 2)
+        softmax_scale = _default_scale(q, softmax_scale)
+        out, lse = _flash_attn_varlen_forward(
+            q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal
+        )
+        if is_grad_enabled and (q.requires_grad or kv.requires_grad):
+            ctx.save_for_backward(q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k)
+            ctx.max_seqlen_q, ctx.max_seqlen_k = max_seqlen_q, max_seqlen_k
+            ctx.softmax_scale, ctx.causal = softmax_scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
+        dq, dk, dv = _flash_attn_varlen_backward(
+            dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
+            ctx.softmax_scale, ctx.causal,
+        )
+        return dq, _repack((dk, dv), 1), None, None, None, None, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# Public functions (interface.py:448-614).
+
+
+def flash_attn_func(q, k, v, softmax_scale: Optional[float] = None, causal: bool = False) -> torch.Tensor:
+    """q (batch, seqlen_q, nheads, headdim); k, v (batch, seqlen_k, nheads_k, headdim).
+    Returns out (batch, seqlen_q, nheads, headdim)."""
+    return FlashAttnFunc.apply(q, k, v, softmax_scale, causal, torch.is_grad_enabled())
+
+
+def flash_attn_qkvpacked_func(qkv, softmax_scale: Optional[float] = None, causal: bool = False) -> torch.Tensor:
+    """qkv (batch, seqlen, 3, nheads, headdim).  Returns out (batch, seqlen, nheads, headdim)."""
+    return FlashAttnQKVPackedFunc.apply(qkv, softmax_scale, causal, torch.is_grad_enabled())
+
+
+def flash_attn_kvpacked_func(q, kv, softmax_scale: Optional[float] = None, causal: bool = False) -> torch.Tensor:
+    """q (batch, seqlen_q, nheads, headdim); kv (batch, seqlen_k, 2, nheads_k, headdim)."""
+    return FlashAttnKVPackedFunc.apply(q, kv, softmax_scale, causal, torch.is_grad_enabled())
+
+
+def flash_attn_varlen_func(
+    q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int,
+    softmax_scale: Optional[float] = None, causal: bool = False,
+) -> torch.Tensor:
+    """q (total_q, nheads, headdim); k, v (total_k, nheads_k, headdim); cu_seqlens_* int32
+    (batch_size + 1,).  Returns out (total_q, nheads, headdim)."""
+    return FlashAttnVarlenFunc.apply(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
+        torch.is_grad_enabled(),
+    )
+
+
+def flash_attn_varlen_qkvpacked_func(
+    qkv, cu_seqlens, max_seqlen: int, softmax_scale: Optional[float] = None, causal: bool = False
+) -> torch.Tensor:
+    """qkv (total, 3, nheads, headdim); cu_seqlens int32 (batch_size + 1,)."""
+    return FlashAttnVarlenQKVPackedFunc.apply(
+        qkv, cu_seqlens, max_seqlen, softmax_scale, causal, torch.is_grad_enabled()
+    )
+
+
+def flash_attn_varlen_kvpacked_func(
+    q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int,
+    softmax_scale: Optional[float] = None, causal: bool = False,
+) -> torch.Tensor:
+    """q (total_q, nheads, headdim); kv (total_k, 2, nheads_k, headdim)."""
+    return FlashAttnVarlenKVPackedFunc.apply(
+        q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
+        torch.is_grad_enabled(),
+    )
+
+
+# ---------------------------------------------------------------------------
+# KV cache (interface.py:617-922).
+
+
+def _validate_unsupported_kvcache_args(rotary_cos, rotary_sin, cache_leftpad, window_size, softcap, alibi_slopes):
+    if rotary_cos is not None or rotary_sin is not None:
+        raise NotImplementedError("Turing KV-cache does not support rotary embeddings yet")
+    if cache_leftpad is not None:
+        raise NotImplementedError("Turing KV-cache does not support cache_leftpad yet")
+    if tuple(window_size) != (-1, -1):
+        raise NotImplementedError("Turing KV-cache does not support local window attention yet")
+    if softcap != 0.0:
+        raise NotImplementedError("Turing KV-cache does not support softcap yet")
+    if alibi_slopes is not None:
+        raise NotImplementedError("Turing KV-cache does not support ALiBi yet")
+
+
+def _validate_supported_head_dim(head_dim: int) -> None:
+    if head_dim not in (64, 128):
+        raise ValueError("Turing FlashAttention supports head_dim 64 or 128")
+
+
+def _cache_capacity(k_cache: torch.Tensor, block_table: Optional[torch.Tensor]) -> int:
+    return k_cache.shape[1] if block_table is None else block_table.shape[1] * k_cache.shape[1]
+
+
+def flash_attn_with_kvcache(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k: Optional[torch.Tensor] = None,
+    v: Optional[torch.Tensor] = None,
+    rotary_cos: Optional[torch.Tensor] = None,
+    rotary_sin: Optional[torch.Tensor] = None,
+    cache_seqlens: Optional[Union[torch.Tensor, int]] = None,
+    cache_batch_idx: Optional[torch.Tensor] = None,
+    cache_leftpad: Optional[torch.Tensor] = None,
+    block_table: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    causal: bool = False,
+    window_size: Tuple[int, int] = (-1, -1),
+    softcap: float = 0.0,
+    rotary_interleaved: bool = True,
+    alibi_slopes: Optional[torch.Tensor] = None,
+    num_splits: int = 0,
+    return_softmax_lse: bool = False,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """KV-cache attention for inference (signature of upstream FlashAttention).
+
+    Supports contiguous caches (optionally remapped by cache_batch_idx), paged
+    caches via block_table, in-place append of k/v at cache_seqlens and split-KV
+    (num_splits, 0 = heuristic).  Rotary, ALiBi, local windows, softcap and
+    cache_leftpad raise NotImplementedError, as in the reference.
+    """
+    # Validation order of interface.py:807-867.
+    _validate_unsupported_kvcache_args(rotary_cos, rotary_sin, cache_leftpad, window_size, softcap, alibi_slopes)
+    if (k is None) != (v is None):
+        raise ValueError("k and v must either both be provided or both be None")
+    _validate_supported_head_dim(q.shape[-1])
+    batch = q.shape[0]
+    if cache_seqlens is None:
+        if k is not None:
+            raise ValueError("cache_seqlens is required when appending k and v")
+        cache_seqlens = torch.full(
+            (batch,), _cache_capacity(k_cache, block_table), dtype=torch.int32, device=k_cache.device
+        )
+    if isinstance(cache_seqlens, int):
+        cache_seqlens = torch.full((batch,), cache_seqlens, dtype=torch.int32, device=k_cache.device)
+    elif not isinstance(cache_seqlens, torch.Tensor):
+        raise TypeError("cache_seqlens must be an int or a torch.Tensor")
+    elif cache_seqlens.dtype != torch.int32:
+        raise TypeError("cache_seqlens must be a torch.int32 tensor")
+    if cache_seqlens.dim() != 1 or cache_seqlens.numel() != batch:
+        raise ValueError("cache_seqlens must have shape [batch_size]")
+    if block_table is not None:
+        if not isinstance(block_table, torch.Tensor):
+            raise TypeError("block_table must be a torch.Tensor")
+        if block_table.dtype != torch.int32:
+            raise TypeError("block_table must be a torch.int32 tensor")
+        if block_table.dim() != 2 or block_table.shape[0] != batch:
+            raise ValueError("block_table must have shape [batch_size, max_num_blocks_per_seq]")
+        if cache_batch_idx is not None:
+            raise NotImplementedError("Paged KV cache does not support cache_batch_idx")
+        if k_cache.shape[1] % 256 != 0:
+            raise ValueError("Paged KV cache block size must be divisible by 256")
+    if cache_batch_idx is not None:
+        if not isinstance(cache_batch_idx, torch.Tensor):
+            raise TypeError("cache_batch_idx must be a torch.Tensor")
+        if cache_batch_idx.dtype != torch.int32:
+            raise TypeError("cache_batch_idx must be a torch.int32 tensor")
+        if cache_batch_idx.dim() != 1 or cache_batch_idx.numel() != batch:
+            raise ValueError("cache_batch_idx must have shape [batch_size]")
+    if num_splits < 0:
+        raise ValueError("num_splits must be non-negative")
+    seqlen_new = 0
+    if k is not None and v is not None:
+        if k.shape[0] != batch or v.shape[0] != batch:
+            raise ValueError("k and v batch size must match q")
+        if k.shape[1] != v.shape[1]:
+            raise ValueError("k and v sequence length must match")
+        seqlen_new = k.shape[1]
+    max_cache_usage = int(cache_seqlens.max().item()) if cache_seqlens.numel() > 0 else 0
+    if max_cache_usage + seqlen_new > _cache_capacity(k_cache, block_table):
+        raise ValueError("cache capacity is insufficient for the requested append length")
+    if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda):
+        raise RuntimeError("q, k_cache, v_cache must be CUDA tensors")
+    if q.dtype != torch.float16 or k_cache.dtype != torch.float16 or v_cache.dtype != torch.float16:
+        raise RuntimeError("q, k_cache, v_cache must be float16 tensors")
+    if k is not None and v is not None:
+        if not (k.is_cuda and v.is_cuda):
+            raise RuntimeError("k and v must be CUDA tensors")
+        if k.dtype != torch.float16 or v.dtype != torch.float16:
+            raise RuntimeError("k and v must be float16 tensors")
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** (-0.5)
+    out, lse = _flash_attn_kvcache_forward(
+        q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale, causal, num_splits
+    )
+    return (out, lse) if return_softmax_lse else out

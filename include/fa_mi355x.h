@@ -1,0 +1,145 @@
+/*
+ * fa_mi355x.h - C ABI of the MI355X (gfx950) FlashAttention kernels.
+ *
+ * This is the boundary between the host layer (the `flash_attn_turing`
+ * PyTorch extension, or any FFI: ctypes, cgo, JNI) and the hand-written HIP
+ * kernels in libfa_mi355x.so.  Every entry point takes plain device pointers,
+ * sizes and strides (in elements, 64-bit), never allocates, launches on the
+ * given HIP stream (a `hipStream_t` passed as `void *`, NULL = default
+ * stream) and returns FA_OK or an error code (see fa_error_string).
+ *
+ * Tensor convention (reference: flash_attention_interface.py:457-462, 530-539;
+ * flash_api.cpp:188-256): q/o [batch][seqlen][heads][head_dim] fp16 with the
+ * last dimension contiguous; k/v [batch][seqlen_k][heads_k][head_dim].  For
+ * packed varlen tensors ([total][heads][head_dim]) batch_stride is ignored and
+ * the row offset of batch b is cu_seqlens[b].  LSE is fp32
+ * [batch][heads][lse_seqlen].  head_dim is 64 or 128 (flash_api.cpp:10-14).
+ * Rows, heads and the base pointer must be 16-byte aligned (strides multiple
+ * of 8 elements).
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    FA_OK = 0,
+    FA_ERR_INVALID_ARG = -1,   /* shape / pointer / alignment check failed   */
+    FA_ERR_UNSUPPORTED = -2,   /* head_dim not in {64, 128} and similar      */
+    FA_ERR_WORKSPACE = -3      /* missing or too small workspace             */
+    /* positive values are hipError_t codes from the launch                  */
+};
+
+/* A strided fp16 tensor [batch][row][head][head_dim]; strides in elements. */
+typedef struct fa_tensor {
+    void *ptr;
+    int64_t batch_stride;
+    int64_t row_stride;
+    int64_t head_stride;
+} fa_tensor;
+
+/*
+ * Forward attention.  Replaces the reference's run_mha_fwd(Flash_fwd_params&)
+ * (flash_api.cpp:174-179, params from set_params_fprop :39-106) used by
+ * mha_fwd (:188-256), mha_varlen_fwd (:353-416) and the KV-cache chunk path
+ * (:686-714).
+ */
+typedef struct fa_fwd_args {
+    fa_tensor q, k, v, o;           /* fp16; o is written for every valid row   */
+    float *lse;                     /* fp32 [batch][nheads][lse_seqlen]          */
+    const int32_t *cu_seqlens_q;    /* [batch+1] or NULL (dense)                 */
+    const int32_t *cu_seqlens_k;    /* [batch+1] or NULL (dense)                 */
+    const int32_t *seqused_k;       /* [batch] keys used per batch, or NULL      */
+    const int32_t *k_batch_idx;     /* [batch] k/v batch read by q batch b, or NULL */
+    int32_t seqused_k_add;          /* added to seqused_k[b] (appended tokens)   */
+    int32_t batch, seqlen_q, seqlen_k, nheads, nheads_k, head_dim;
+    int32_t lse_seqlen;             /* seqlen_q, or max_seqlen_q for varlen      */
+    float softmax_scale;
+    int32_t causal;                 /* bottom-right aligned (mask.h:52)          */
+} fa_fwd_args;
+
+int fa_fwd(const fa_fwd_args *args, void *stream);
+
+/*
+ * Backward attention.  Replaces run_mha_bwd(Flash_bwd_params&) (flash_api.cpp:181-186)
+ * and run_flash_bwd's three launches (flash_bwd_launch_template.h:69-146), plus
+ * the GQA dK/dV reduction done with torch::sum_out (flash_api.cpp:338-348,
+ * 493-503): dk/dv are written per KV head, the group is summed in-kernel.
+ */
+typedef struct fa_bwd_args {
+    fa_tensor q, k, v, o, dout;     /* fp16 inputs                               */
+    fa_tensor dq, dk, dv;           /* fp16 outputs, every valid row written     */
+    const float *lse;               /* fp32 [batch][nheads][lse_seqlen]          */
+    float *dsum;                    /* workspace fp32 [batch][nheads][lse_seqlen] = rowsum(dO*O) */
+    const int32_t *cu_seqlens_q;
+    const int32_t *cu_seqlens_k;
+    int32_t batch, seqlen_q, seqlen_k, nheads, nheads_k, head_dim;
+    int32_t lse_seqlen;
+    float softmax_scale;
+    int32_t causal;
+} fa_bwd_args;
+
+/* D = rowsum(dO * O) (flash_bwd_preprocess_kernel.h:23-96). */
+int fa_bwd_preprocess(const fa_bwd_args *args, void *stream);
+/* dQ kernel (flash_bwd_kernel.h:25-609); needs dsum from fa_bwd_preprocess. */
+int fa_bwd_dq(const fa_bwd_args *args, void *stream);
+/* dK/dV kernel with in-kernel GQA accumulation (flash_bwd_kernel.h:613-1344). */
+int fa_bwd_dkdv(const fa_bwd_args *args, void *stream);
+/* preprocess + dQ + dK/dV in stream order. */
+int fa_bwd(const fa_bwd_args *args, void *stream);
+
+/*
+ * KV-cache attention.  Replaces run_kvcache_paged_append (kvcache_native.cu:956-993),
+ * the contiguous append loop (flash_api.cpp:643-654) and run_mha_fwd_kvcache_native
+ * (kvcache_native.cu:995-1218) called from mha_fwd_kvcache (flash_api.cpp:508-715).
+ * Attention runs over L_b = cache_seqlens[b] + seqlen_new keys.
+ */
+typedef struct fa_kvcache_args {
+    fa_tensor q;                    /* [batch][seqlen_q][nheads][head_dim]       */
+    fa_tensor k_cache, v_cache;     /* contiguous [batch_cache][capacity][nheads_k][d]
+                                       or paged [num_blocks][page_block_size][nheads_k][d] */
+    fa_tensor k_new, v_new;         /* [batch][seqlen_new][nheads_k][d]; ptr NULL = no append */
+    fa_tensor o;                    /* [batch][seqlen_q][nheads][head_dim]       */
+    float *lse;                     /* [batch][nheads][seqlen_q]                 */
+    const int32_t *cache_seqlens;   /* [batch] tokens in the cache before append */
+    const int32_t *cache_batch_idx; /* [batch] cache row of batch b, or NULL     */
+    const int32_t *block_table;     /* [batch][block_table_stride], or NULL      */
+    int64_t block_table_stride;
+    int32_t batch, seqlen_q, nheads, nheads_k, head_dim;
+    int32_t seqlen_new;             /* tokens appended per sequence (0 = none)   */
+    int32_t page_block_size;        /* paged: multiple of 256; contiguous: 0     */
+    int32_t num_splits;             /* >= 1, as resolved by fa_kv_num_splits     */
+    float softmax_scale;
+    int32_t causal;
+    float *out_accum;               /* workspace [num_splits][batch*nheads*seqlen_q][d] fp32 */
+    float *lse_accum;               /* workspace [num_splits][batch*nheads*seqlen_q] fp32    */
+} fa_kvcache_args;
+
+/* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);
+ * requested > 0 is returned unchanged. */
+int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seqlen_q,
+                     int batch, int nheads, int nheads_k, int num_cus);
+/* Workspace bytes fa_kv_splitkv needs for args->num_splits (0 when num_splits == 1). */
+size_t fa_kv_workspace_bytes(const fa_kvcache_args *args);
+/* In-place append of k_new/v_new at cache_seqlens (contiguous, remapped or paged). */
+int fa_kv_append(const fa_kvcache_args *args, void *stream);
+/* Split-KV partial attention; writes o/lse directly when num_splits == 1. */
+int fa_kv_splitkv(const fa_kvcache_args *args, void *stream);
+/* Log-sum-exp combine of the split partials into o/lse (kvcache_native.cu:676-729). */
+int fa_kv_combine(const fa_kvcache_args *args, void *stream);
+/* append + split-KV + combine in stream order. */
+int fa_fwd_kvcache(const fa_kvcache_args *args, void *stream);
+
+/* Human-readable text for a return code (FA_* or hipError_t). */
+const char *fa_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */

@@ -1,0 +1,174 @@
+"""KV-cache oracle (CPU).  Test infrastructure only.
+
+Restates the reference's own Python math path for ``flash_attn_with_kvcache``
+(flash_attention_interface.py:642-776) and the split / combine arithmetic of
+csrc/flash_attn/src/kvcache_native.cu:191-193 (split bounds), :676-729
+(log-sum-exp combine) and :782-871 (paged append).
+"""
+
+from typing import List, Optional, Tuple
+
+import torch
+
+from .attention import causal_keep
+
+
+def append_contiguous(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    cache_batch_idx: Optional[torch.Tensor] = None,
+) -> None:
+    """In place: k/v[b, t] -> cache row ``cache_batch_idx[b]`` (or b) at
+    position ``cache_seqlens[b] + t`` (flash_attention_interface.py:642-662,
+    flash_api.cpp:643-654)."""
+    starts = [int(x) for x in cache_seqlens.tolist()]
+    rows = (
+        [int(x) for x in cache_batch_idx.tolist()]
+        if cache_batch_idx is not None
+        else list(range(k.shape[0]))
+    )
+    n = k.shape[1]
+    for bi, start in enumerate(starts):
+        k_cache[rows[bi], start : start + n] = k[bi]
+        v_cache[rows[bi], start : start + n] = v[bi]
+
+
+def append_paged(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    block_table: torch.Tensor,
+) -> None:
+    """In place: logical position p = cache_seqlens[b] + t goes to physical page
+    block_table[b, p // page] at offset p % page
+    (flash_attention_interface.py:665-685, kvcache_native.cu:825-839)."""
+    page = k_cache.shape[1]
+    starts = [int(x) for x in cache_seqlens.tolist()]
+    table = block_table.tolist()
+    for bi, start in enumerate(starts):
+        for t in range(k.shape[1]):
+            pos = start + t
+            blk = table[bi][pos // page]
+            k_cache[blk, pos % page] = k[bi, t]
+            v_cache[blk, pos % page] = v[bi, t]
+
+
+def materialize(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    seqlens: torch.Tensor,
+    cache_batch_idx: Optional[torch.Tensor],
+    block_table: Optional[torch.Tensor],
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Logical per-sequence K/V [b, max_len, hk, d] read through the remap or the
+    page table, zero past each length (flash_attention_interface.py:688-728)."""
+    lens = [int(x) for x in seqlens.tolist()]
+    max_len = max(lens) if lens else 0
+    b = len(lens)
+    hk, d = k_cache.shape[2], k_cache.shape[3]
+    k_out = torch.zeros((b, max_len, hk, d), dtype=k_cache.dtype)
+    v_out = torch.zeros_like(k_out)
+    if block_table is None:
+        rows = (
+            [int(x) for x in cache_batch_idx.tolist()]
+            if cache_batch_idx is not None
+            else list(range(b))
+        )
+        for bi, n in enumerate(lens):
+            k_out[bi, :n] = k_cache[rows[bi], :n]
+            v_out[bi, :n] = v_cache[rows[bi], :n]
+        return k_out, v_out
+    page = k_cache.shape[1]
+    table = block_table.tolist()
+    for bi, n in enumerate(lens):
+        pos = 0
+        while pos < n:
+            blk = table[bi][pos // page]
+            off = pos % page
+            take = min(page - off, n - pos)
+            k_out[bi, pos : pos + take] = k_cache[blk, off : off + take]
+            v_out[bi, pos : pos + take] = v_cache[blk, off : off + take]
+            pos += take
+    return k_out, v_out
+
+
+def split_bounds(seqlen_k: int, num_splits: int) -> List[Tuple[int, int]]:
+    """Split s of S covers [L*s // S, L*(s+1) // S) (kvcache_native.cu:191-192,
+    flash_attention_interface.py:755-756)."""
+    return [((seqlen_k * s) // num_splits, (seqlen_k * (s + 1)) // num_splits) for s in range(num_splits)]
+
+
+def combine(out_parts: torch.Tensor, lse_parts: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Log-sum-exp combine of split partials (kvcache_native.cu:697-727).
+
+    out_parts [S, rows, d] (already normalised per split), lse_parts [S, rows]
+    with -inf for an empty split.  Returns (out [rows, d], lse [rows]) with the
+    LSE of an all-empty row reported as 0 and its output 0."""
+    lse_max = lse_parts.max(dim=0).values
+    finite = torch.isfinite(lse_max)
+    shift = torch.where(finite, lse_max, torch.zeros_like(lse_max))
+    w_sum = torch.exp(lse_parts - shift[None]).sum(dim=0)
+    lse_tot = torch.where(finite & (w_sum > 0), shift + torch.log(w_sum), torch.full_like(shift, float("-inf")))
+    ok = torch.isfinite(lse_tot)
+    w = torch.exp(lse_parts - torch.where(ok, lse_tot, torch.zeros_like(lse_tot))[None])
+    w = torch.where(ok[None], w, torch.zeros_like(w))
+    out = (w[..., None] * out_parts).sum(dim=0)
+    return out, torch.where(ok, lse_tot, torch.zeros_like(lse_tot))
+
+
+def splitkv_attention(
+    q: torch.Tensor,
+    k_used: torch.Tensor,
+    v_used: torch.Tensor,
+    seqlens: torch.Tensor,
+    softmax_scale: float,
+    causal: bool,
+    num_splits: int,
+    dtype: torch.dtype = torch.float32,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Split-KV attention over materialised caches, per batch row
+    (flash_attention_interface.py:731-776): each split is a separate softmax
+    with its own LSE (-inf when empty), then the log-sum-exp combine.
+
+    q [b, sq, h, d]; k_used/v_used [b, >=max_len, hk, d]; causal keeps key j for
+    query i iff j <= i + L - sq with L = seqlens[b] (kvcache_native.cu:347).
+    Returns (out [b, sq, h, d] in ``dtype``, lse [b, h, sq] in ``dtype``)."""
+    b, sq, h, d = q.shape
+    hk = k_used.shape[2]
+    groups = h // hk
+    out = torch.zeros((b, sq, h, d), dtype=dtype)
+    lse = torch.zeros((b, h, sq), dtype=dtype)
+    for bi, n in enumerate(int(x) for x in seqlens.tolist()):
+        qi = q[bi].to(dtype).transpose(0, 1)  # h sq d
+        ki = k_used[bi, :n].to(dtype).repeat_interleave(groups, dim=1).transpose(0, 1)
+        vi = v_used[bi, :n].to(dtype).repeat_interleave(groups, dim=1).transpose(0, 1)
+        splits = max(1, min(num_splits, n)) if num_splits > 0 else 1
+        keep = causal_keep(sq, n) if causal else torch.ones((sq, n), dtype=torch.bool)
+        parts_o, parts_l = [], []
+        for s0, s1 in split_bounds(n, splits):
+            sc = torch.matmul(qi, ki[:, s0:s1].transpose(-1, -2).contiguous()) * softmax_scale
+            sc = sc.masked_fill(~keep[:, s0:s1], float("-inf"))
+            any_row = torch.isfinite(sc).any(dim=-1, keepdim=True) if s1 > s0 else torch.zeros(
+                (h, sq, 1), dtype=torch.bool
+            )
+            if s1 > s0:
+                m = torch.where(any_row, sc.amax(dim=-1, keepdim=True), torch.zeros_like(sc[..., :1]))
+                p = torch.exp(sc - m)
+                l = p.sum(dim=-1, keepdim=True)
+                safe = torch.where(l > 0, l, torch.ones_like(l))
+                o = torch.where(any_row, torch.matmul(p / safe, vi[:, s0:s1]), torch.zeros((h, sq, d), dtype=dtype))
+                lp = torch.where(any_row, m + torch.log(safe), torch.full_like(m, float("-inf"))).squeeze(-1)
+            else:
+                o = torch.zeros((h, sq, d), dtype=dtype)
+                lp = torch.full((h, sq), float("-inf"), dtype=dtype)
+            parts_o.append(o.reshape(h * sq, d))
+            parts_l.append(lp.reshape(h * sq))
+        o_tot, l_tot = combine(torch.stack(parts_o), torch.stack(parts_l))
+        out[bi] = o_tot.reshape(h, sq, d).transpose(0, 1)
+        lse[bi] = l_tot.reshape(h, sq)
+    return out, lse

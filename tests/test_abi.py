@@ -1,0 +1,57 @@
+"""The C-ABI library loads and exports every entry point include/fa_mi355x.h
+declares (CPU only: no compute calls), and argument errors come back as codes."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fa_mi355x.h")
+LIB = os.path.join(REPO, "flash-attention-turing_amd", "libfa_mi355x.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_]+\s*\*?\s*(fa_[a-z0-9_]+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch  # noqa: F401  (HIP runtime first, as in every product import)
+
+    assert os.path.exists(LIB), "libfa_mi355x.so is not built (python __graft_entry__.py / build.py)"
+    return ctypes.CDLL(LIB)
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    for required in ("fa_fwd", "fa_bwd_preprocess", "fa_bwd_dq", "fa_bwd_dkdv", "fa_bwd", "fa_kv_append",
+                     "fa_kv_splitkv", "fa_kv_combine", "fa_fwd_kvcache", "fa_kv_num_splits",
+                     "fa_kv_workspace_bytes", "fa_error_string"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in fa_mi355x.h but not exported"
+
+
+def test_argument_errors_are_codes(lib):
+    lib.fa_error_string.restype = ctypes.c_char_p
+    assert lib.fa_fwd(None, None) == -1
+    assert lib.fa_bwd(None, None) == -1
+    assert lib.fa_fwd_kvcache(None, None) == -1
+    assert b"invalid argument" in lib.fa_error_string(-1)
+    assert b"head_dim" in lib.fa_error_string(-2)
+
+
+def test_num_splits_heuristic(lib):
+    f = lib.fa_kv_num_splits
+    assert f(7, 100000, 128, 1, 64, 32, 8, 256) == 7  # explicit requests are kept
+    assert f(0, 256, 128, 1, 1, 8, 8, 256) == 1  # too short to split
+    s = f(0, 32768, 128, 1, 4, 32, 8, 256)
+    assert 1 < s <= 64
+    assert f(0, 1 << 20, 128, 1, 1, 8, 1, 256) <= 128

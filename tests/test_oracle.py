@@ -1,0 +1,267 @@
+"""Pins the CPU oracle before it is trusted as the parity reference.
+
+The reference ships no golden vectors for this path (its tests compare against
+runtime SDPA on unseeded inputs), so every oracle function is checked against
+something independent of its own formula:
+  * closed forms: sq = sk = 1, constant keys (uniform softmax), a dominant key,
+    fully masked rows, the bottom-right causal alignment with sq != sk;
+  * float64 brute force written as plain loops over the definitions;
+  * torch.autograd of an independently written expression, and central finite
+    differences, for the backward;
+  * exact invariants for the cache functions (slice writes, page-table
+    round trips, split-KV == unsplit, a hand-computed combine).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import kvcache as okv
+from oracle import twin
+from oracle.attention import attention_bwd, attention_fwd, causal_keep, varlen_bwd, varlen_fwd
+
+D64 = torch.float64
+
+
+def _rand(shape, seed, dtype=D64):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+def _brute_fwd(q, k, v, scale, causal):
+    """Plain loops over the definition of softmax attention (bottom-right causal)."""
+    b, sq, h, d = q.shape
+    sk, hk = k.shape[1], k.shape[2]
+    grp = h // hk
+    out = torch.zeros(b, sq, h, d, dtype=D64)
+    lse = torch.zeros(b, h, sq, dtype=D64)
+    for bi in range(b):
+        for hi in range(h):
+            kh = hi // grp
+            for i in range(sq):
+                logits = []
+                for j in range(sk):
+                    if causal and j > i + sk - sq:
+                        continue
+                    dot = sum(float(q[bi, i, hi, t]) * float(k[bi, j, kh, t]) for t in range(d))
+                    logits.append((j, dot * scale))
+                if not logits:
+                    continue
+                m = max(x for _, x in logits)
+                z = sum(math.exp(x - m) for _, x in logits)
+                lse[bi, hi, i] = m + math.log(z)
+                for j, x in logits:
+                    out[bi, i, hi] += math.exp(x - m) / z * v[bi, j, kh].double()
+    return out, lse
+
+
+def test_fwd_single_token_closed_form():
+    q, k, v = _rand((1, 1, 2, 8), 1), _rand((1, 1, 2, 8), 2), _rand((1, 1, 2, 8), 3)
+    out, lse = attention_fwd(q, k, v, 0.37, False, dtype=D64)
+    assert torch.allclose(out, v, atol=1e-14)
+    assert torch.allclose(lse[0, :, 0], 0.37 * (q[0, 0] * k[0, 0]).sum(-1), atol=1e-14)
+
+
+def test_fwd_constant_keys_give_prefix_means_bottom_right():
+    # Identical keys -> uniform weights over the visible keys.  sq=2, sk=3 causal:
+    # row 0 sees keys 0..1, row 1 sees keys 0..2 (bottom-right, mask.h:52).
+    q = _rand((1, 2, 1, 4), 4)
+    k = _rand((1, 1, 1, 4), 5).expand(1, 3, 1, 4).contiguous()
+    v = _rand((1, 3, 1, 4), 6)
+    out, _ = attention_fwd(q, k, v, 1.0, True, dtype=D64)
+    assert torch.allclose(out[0, 0, 0], v[0, :2, 0].mean(0), atol=1e-14)
+    assert torch.allclose(out[0, 1, 0], v[0, :3, 0].mean(0), atol=1e-14)
+    out_nc, _ = attention_fwd(q, k, v, 1.0, False, dtype=D64)
+    assert torch.allclose(out_nc[0, 0, 0], v[0, :, 0].mean(0), atol=1e-14)
+
+
+def test_fwd_dominant_key():
+    q = torch.zeros(1, 1, 1, 4, dtype=D64)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, 5, 1, 4, dtype=D64)
+    k[0, 3, 0, 0] = 80.0
+    v = _rand((1, 5, 1, 4), 7)
+    out, lse = attention_fwd(q, k, v, 1.0, False, dtype=D64)
+    assert torch.allclose(out[0, 0, 0], v[0, 3, 0], atol=1e-12)
+    assert abs(lse.item() - 80.0) < 1e-12
+
+
+def test_fwd_fully_masked_rows_are_zero():
+    q, k, v = _rand((1, 5, 2, 4), 8), _rand((1, 2, 1, 4), 9), _rand((1, 2, 1, 4), 10)
+    out, lse = attention_fwd(q, k, v, 0.5, True, dtype=D64)
+    assert torch.all(out[0, :3] == 0) and torch.all(lse[0, :, :3] == 0)
+    assert torch.all(out[0, 3:] != 0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,sk", [(3, 4), (4, 3), (1, 5), (5, 5)])
+def test_fwd_matches_brute_force(causal, sq, sk):
+    q, k, v = _rand((2, sq, 4, 6), 11), _rand((2, sk, 2, 6), 12), _rand((2, sk, 2, 6), 13)
+    out, lse = attention_fwd(q, k, v, 0.41, causal, dtype=D64)
+    bo, bl = _brute_fwd(q, k, v, 0.41, causal)
+    assert torch.allclose(out, bo, atol=1e-12)
+    assert torch.allclose(lse, bl, atol=1e-12)
+
+
+def _autograd_ref(q, k, v, do, scale, causal):
+    """An independent expression (softmax + matmul, repeat for GQA) differentiated by autograd."""
+    q, k, v = (t.clone().requires_grad_() for t in (q, k, v))
+    grp = q.shape[2] // k.shape[2]
+    kk = k.repeat_interleave(grp, dim=2)
+    vv = v.repeat_interleave(grp, dim=2)
+    s = torch.einsum("bihd,bjhd->bhij", q, kk) * scale
+    if causal:
+        s = s.masked_fill(~causal_keep(q.shape[1], k.shape[1]), float("-inf"))
+    p = torch.softmax(s, dim=-1).nan_to_num(0.0)
+    o = torch.einsum("bhij,bjhd->bihd", p, vv)
+    o.backward(do)
+    return q.grad, k.grad, v.grad
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,sk,h,hk", [(5, 7, 2, 1), (7, 5, 4, 2), (6, 6, 3, 3)])
+def test_bwd_matches_autograd(causal, sq, sk, h, hk):
+    q, k, v = _rand((2, sq, h, 8), 14), _rand((2, sk, hk, 8), 15), _rand((2, sk, hk, 8), 16)
+    do = _rand((2, sq, h, 8), 17)
+    out, lse = attention_fwd(q, k, v, 0.3, causal, dtype=D64)
+    dq, dk, dv = attention_bwd(q, k, v, out, lse, do, 0.3, causal, dtype=D64)
+    rq, rk, rv = _autograd_ref(q, k, v, do, 0.3, causal)
+    assert torch.allclose(dq, rq, atol=1e-12)
+    assert torch.allclose(dk, rk, atol=1e-12)
+    assert torch.allclose(dv, rv, atol=1e-12)
+
+
+def test_bwd_finite_differences():
+    q, k, v = _rand((1, 4, 2, 4), 18), _rand((1, 6, 1, 4), 19), _rand((1, 6, 1, 4), 20)
+    do = _rand((1, 4, 2, 4), 21)
+    out, lse = attention_fwd(q, k, v, 0.7, True, dtype=D64)
+    grads = attention_bwd(q, k, v, out, lse, do, 0.7, True, dtype=D64)
+
+    def loss(qq, kk, vv):
+        return (attention_fwd(qq, kk, vv, 0.7, True, dtype=D64)[0] * do).sum().item()
+
+    eps = 1e-6
+    for gi, t in enumerate((q, k, v)):
+        for idx in [(0, 1, 0, 2), (0, 3, 0, 0), (0, 2, 0, 3)]:
+            if idx[2] >= t.shape[2]:
+                continue
+            tp, tm = t.clone(), t.clone()
+            tp[idx] += eps
+            tm[idx] -= eps
+            args_p = [q, k, v]
+            args_m = [q, k, v]
+            args_p[gi], args_m[gi] = tp, tm
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
+            assert abs(fd - grads[gi][idx].item()) < 1e-7
+
+
+def test_varlen_equals_dense_per_sequence():
+    lens = [3, 5, 1]
+    cu = torch.tensor([0, 3, 8, 9], dtype=torch.int32)
+    q, k, v = _rand((9, 2, 4), 22), _rand((9, 1, 4), 23), _rand((9, 1, 4), 24)
+    do = _rand((9, 2, 4), 25)
+    out, lse = varlen_fwd(q, k, v, cu, cu, 5, 0.5, True, dtype=D64)
+    assert lse.shape == (3, 2, 5)
+    assert torch.all(lse[0, :, 3:] == 0) and torch.all(lse[2, :, 1:] == 0)
+    grads = varlen_bwd(q, k, v, out, lse, do, cu, cu, 0.5, True, dtype=D64)
+    for bi, (a, n) in enumerate(zip([0, 3, 8], lens)):
+        bo, bl = _brute_fwd(q[a : a + n][None], k[a : a + n][None], v[a : a + n][None], 0.5, True)
+        assert torch.allclose(out[a : a + n], bo[0], atol=1e-12)
+        assert torch.allclose(lse[bi, :, :n], bl[0], atol=1e-12)
+        rq, rk, rv = _autograd_ref(q[a : a + n][None], k[a : a + n][None], v[a : a + n][None], do[a : a + n][None], 0.5, True)
+        assert torch.allclose(grads[0][a : a + n], rq[0], atol=1e-12)
+        assert torch.allclose(grads[1][a : a + n], rk[0], atol=1e-12)
+
+
+# --------------------------------------------------------------------------- kv cache
+
+
+def test_append_contiguous_and_remap_are_slice_writes():
+    kc = torch.zeros(4, 10, 2, 8, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    k = _rand((2, 3, 2, 8), 26, torch.float16)
+    v = _rand((2, 3, 2, 8), 27, torch.float16)
+    okv.append_contiguous(kc, vc, k, v, torch.tensor([2, 7], dtype=torch.int32), torch.tensor([3, 0], dtype=torch.int32))
+    assert torch.equal(kc[3, 2:5], k[0]) and torch.equal(kc[0, 7:10], k[1]) and torch.equal(vc[0, 7:10], v[1])
+    assert kc[1].abs().sum() == 0 and kc[2].abs().sum() == 0 and kc[3, :2].abs().sum() == 0
+
+
+def test_append_paged_roundtrip_equals_contiguous():
+    g = torch.Generator().manual_seed(28)
+    b, cap, page = 3, 768, 256
+    kc = _rand((b, cap, 1, 8), 29, torch.float16)
+    vc = _rand((b, cap, 1, 8), 30, torch.float16)
+    lens = torch.tensor([0, 255, 700], dtype=torch.int32)
+    k = _rand((b, 4, 1, 8), 31, torch.float16)
+    v = _rand((b, 4, 1, 8), 32, torch.float16)
+    perm = torch.randperm(b * 3, generator=g)
+    table = perm.reshape(b, 3).to(torch.int32)
+    kp = torch.zeros(b * 3, page, 1, 8, dtype=torch.float16)
+    vp = torch.zeros_like(kp)
+    for bi in range(b):
+        for j in range(3):
+            kp[table[bi, j]] = kc[bi, j * page : (j + 1) * page]
+            vp[table[bi, j]] = vc[bi, j * page : (j + 1) * page]
+    okv.append_contiguous(kc, vc, k, v, lens, None)
+    okv.append_paged(kp, vp, k, v, lens, table)
+    a = okv.materialize(kc, vc, lens + 4, None, None)
+    bmat = okv.materialize(kp, vp, lens + 4, None, table)
+    assert torch.equal(a[0], bmat[0]) and torch.equal(a[1], bmat[1])
+    # position 255 + t crosses the page boundary 255 | 256
+    assert torch.equal(bmat[0][1, 255:259], k[1])
+
+
+def test_split_bounds_partition():
+    for L in [0, 1, 7, 1000, 4097]:
+        for S in [1, 3, 8, 16]:
+            bnd = okv.split_bounds(L, S)
+            assert bnd[0][0] == 0 and bnd[-1][1] == L
+            assert all(bnd[i][1] == bnd[i + 1][0] for i in range(S - 1))
+
+
+def test_combine_known_answer():
+    # Two splits with lse a, b: weights e^a / (e^a + e^b), e^b / (e^a + e^b).
+    out_parts = torch.tensor([[[1.0, 0.0]], [[0.0, 3.0]]], dtype=D64)
+    lse_parts = torch.tensor([[math.log(1.0)], [math.log(3.0)]], dtype=D64)
+    out, lse = okv.combine(out_parts, lse_parts)
+    assert torch.allclose(out[0], torch.tensor([0.25, 2.25], dtype=D64), atol=1e-15)
+    assert abs(lse.item() - math.log(4.0)) < 1e-15
+    # an empty split (-inf) has weight 0; an all-empty row reports 0 / 0
+    out, lse = okv.combine(torch.ones(2, 2, 2, dtype=D64), torch.tensor([[0.0, -math.inf], [-math.inf, -math.inf]], dtype=D64))
+    assert torch.allclose(out[0], torch.ones(2, dtype=D64)) and torch.all(out[1] == 0) and lse[1] == 0
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_splitkv_equals_unsplit_and_dense(causal):
+    q = _rand((3, 2, 4, 8), 33)
+    ku, vu = _rand((3, 40, 2, 8), 34), _rand((3, 40, 2, 8), 35)
+    lens = torch.tensor([40, 1, 23], dtype=torch.int32)
+    o1, l1 = okv.splitkv_attention(q, ku, vu, lens, 0.3, causal, 1, dtype=D64)
+    for S in (2, 5, 16, 64):
+        oS, lS = okv.splitkv_attention(q, ku, vu, lens, 0.3, causal, S, dtype=D64)
+        assert torch.allclose(oS, o1, atol=1e-12) and torch.allclose(lS, l1, atol=1e-12)
+    for bi, n in enumerate(lens.tolist()):
+        bo, bl = _brute_fwd(q[bi : bi + 1], ku[bi : bi + 1, :n], vu[bi : bi + 1, :n], 0.3, causal)
+        assert torch.allclose(o1[bi], bo[0], atol=1e-12) and torch.allclose(l1[bi], bl[0], atol=1e-12)
+
+
+# --------------------------------------------------------------------------- twin
+
+
+def test_twin_rounds_where_the_reference_rounds():
+    q, k, v = (_rand((1, 1, 1, 64), s, torch.float16) for s in (36, 37, 38))
+    out, lse = twin.fwd_twin(q, k, v, 0.125, False)
+    assert torch.equal(out, v)  # P = 1 exactly, O = V
+    q, k, v = (_rand((2, 300, 4, 128), s, torch.float16) for s in (39, 40, 41))
+    o_tw, l_tw = twin.fwd_twin(q, k, v, 128 ** -0.5, True)
+    o_ref, l_ref = attention_fwd(q, k, v, 128 ** -0.5, True)
+    err = (o_tw.float() - o_ref).abs().max().item()
+    assert 1e-5 < err < 5e-3  # rounding points present, but small
+    assert (l_tw - l_ref).abs().max().item() < 1e-4
+    do = _rand((2, 300, 4, 128), 42, torch.float16)
+    g_tw = twin.bwd_twin(q, k, v, o_tw, l_tw, do, 128 ** -0.5, True)
+    g_ref = attention_bwd(q, k, v, o_ref, l_ref, do, 128 ** -0.5, True)
+    for a, b in zip(g_tw, g_ref):
+        e = (a.float() - b).abs().max().item()
+        assert 1e-5 < e < 2e-2

@@ -1,0 +1,75 @@
+"""Varlen (packed) forward + backward parity on the GPU against the per-sequence
+fp32 oracle (test_flash_attn.py:467-503 restated), 2x-twin bounds, and the LSE
+layout [b, h, max_seqlen_q] with zero padding (flash_api.cpp:388)."""
+
+import pytest
+import torch
+
+import flash_attention_interface as fai
+from helpers import assert_2x, assert_lse, cu_from_lengths, randn16
+from oracle.attention import attention_bwd, attention_fwd
+from oracle.twin import bwd_twin, fwd_twin
+
+CASES = [
+    # lengths_q, lengths_k, h, hk, hd, causal
+    ([128, 1, 300, 77], None, 4, 2, 64, True),
+    ([513, 64, 129], None, 8, 2, 128, True),
+    ([200, 17, 90], [100, 300, 90], 6, 3, 128, False),
+    ([200, 17, 90], [100, 300, 90], 4, 1, 64, True),
+    ([1, 1, 1], [50, 0, 3], 2, 2, 128, False),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens_q,lens_k,h,hk,hd,causal", CASES)
+def test_varlen_parity(device, lens_q, lens_k, h, hk, hd, causal):
+    lens_k = lens_k or lens_q
+    g = torch.Generator().manual_seed(3000 + sum(lens_q) + hd)
+    cu_q, cu_k = cu_from_lengths(lens_q), cu_from_lengths(lens_k)
+    tq, tk = int(cu_q[-1]), int(cu_k[-1])
+    q = randn16((tq, h, hd), g)
+    k = randn16((tk, hk, hd), g)
+    v = randn16((tk, hk, hd), g)
+    do = randn16((tq, h, hd), g)
+    s = hd ** -0.5
+    mq, mk = max(lens_q), max(lens_k)
+    qd, kd, vd = (t.to(device).requires_grad_() for t in (q, k, v))
+    out, lse = fai._flash_attn_varlen_forward(qd, kd, vd, cu_q.to(device), cu_k.to(device), mq, mk, s, causal)
+    dq, dk, dv = fai._flash_attn_varlen_backward(
+        do.to(device), qd, kd, vd, out, lse, cu_q.to(device), cu_k.to(device), mq, mk, s, causal
+    )
+    torch.cuda.synchronize()
+    assert lse.shape == (len(lens_q), h, mq)
+    o_ref = torch.zeros(q.shape)
+    o_tw = torch.zeros(q.shape, dtype=torch.float16)
+    g_ref = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
+    g_tw = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
+    lse_ref = torch.zeros((len(lens_q), h, mq))
+    for b in range(len(lens_q)):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        qb, kb, vb, dob = q[q0:q1][None], k[k0:k1][None], v[k0:k1][None], do[q0:q1][None]
+        ob, lb = attention_fwd(qb, kb, vb, s, causal)
+        otb, ltb = fwd_twin(qb, kb, vb, s, causal)
+        o_ref[q0:q1], o_tw[q0:q1], lse_ref[b, :, : q1 - q0] = ob[0], otb[0], lb[0]
+        gr = attention_bwd(qb, kb, vb, ob, lb, dob, s, causal)
+        gt = bwd_twin(qb, kb, vb, otb, ltb, dob, s, causal)
+        for i, (lo, hi) in enumerate([(q0, q1), (k0, k1), (k0, k1)]):
+            g_ref[i][lo:hi], g_tw[i][lo:hi] = gr[i][0], gt[i][0].float()
+    assert_2x("out", out, o_ref, o_tw)
+    assert_lse(lse, lse_ref)  # includes the zero padding past each length
+    for name, got, r, t in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref, g_tw):
+        assert_2x(name, got, r, t)
+
+
+@pytest.mark.gpu
+def test_varlen_public_packed_variants(device):
+    g = torch.Generator().manual_seed(31)
+    lens = [100, 37, 260]
+    cu = cu_from_lengths(lens).to(device)
+    qkv = randn16((sum(lens), 3, 4, 64), g).to(device)
+    out_p = fai.flash_attn_varlen_qkvpacked_func(qkv, cu, max(lens), causal=True)
+    q, k, v = (qkv[:, i] for i in range(3))
+    out = fai.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal=True)
+    assert torch.equal(out_p, out)
+    out_kv = fai.flash_attn_varlen_kvpacked_func(q, qkv[:, 1:], cu, cu, max(lens), max(lens), causal=True)
+    assert torch.equal(out_kv, out)
