@@ -1,0 +1,194 @@
+"""ctypes binding of the C ABI in include/fa_mi355x.h (libfa_mi355x.so).
+
+This is the binding a non-torch host (or a maintainer wiring the library into
+another runtime) would write: plain structs of device pointers, sizes and
+strides, a stream handle and an int return code.  ``bench.py`` and the
+C-ABI parity tests use it to launch the kernels one by one; the drop-in
+Python API goes through the ``flash_attn_turing`` extension instead, which
+calls the same entry points from C++.
+
+Tensors are passed as torch tensors only for convenience: ``tensor_desc``
+reads their data pointer and strides.  Nothing here allocates device memory.
+"""
+
+import ctypes
+import os
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfa_mi355x.so")
+
+FA_OK = 0
+FA_ERR_INVALID_ARG = -1
+FA_ERR_UNSUPPORTED = -2
+FA_ERR_WORKSPACE = -3
+
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_p = ctypes.c_void_p
+
+
+class FaTensor(ctypes.Structure):
+    _fields_ = [("ptr", _p), ("batch_stride", _i64), ("row_stride", _i64), ("head_stride", _i64)]
+
+
+class FaFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", FaTensor), ("k", FaTensor), ("v", FaTensor), ("o", FaTensor),
+        ("lse", _p), ("cu_seqlens_q", _p), ("cu_seqlens_k", _p), ("seqused_k", _p), ("k_batch_idx", _p),
+        ("seqused_k_add", _i32),
+        ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32), ("nheads", _i32), ("nheads_k", _i32),
+        ("head_dim", _i32), ("lse_seqlen", _i32), ("softmax_scale", _f32), ("causal", _i32),
+    ]
+
+
+class FaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", FaTensor), ("k", FaTensor), ("v", FaTensor), ("o", FaTensor), ("dout", FaTensor),
+        ("dq", FaTensor), ("dk", FaTensor), ("dv", FaTensor),
+        ("lse", _p), ("dsum", _p), ("cu_seqlens_q", _p), ("cu_seqlens_k", _p),
+        ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32), ("nheads", _i32), ("nheads_k", _i32),
+        ("head_dim", _i32), ("lse_seqlen", _i32), ("softmax_scale", _f32), ("causal", _i32),
+    ]
+
+
+class FaKvcacheArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", FaTensor), ("k_cache", FaTensor), ("v_cache", FaTensor), ("k_new", FaTensor), ("v_new", FaTensor),
+        ("o", FaTensor), ("lse", _p), ("cache_seqlens", _p), ("cache_batch_idx", _p), ("block_table", _p),
+        ("block_table_stride", _i64),
+        ("batch", _i32), ("seqlen_q", _i32), ("nheads", _i32), ("nheads_k", _i32), ("head_dim", _i32),
+        ("seqlen_new", _i32), ("page_block_size", _i32), ("num_splits", _i32), ("softmax_scale", _f32),
+        ("causal", _i32), ("out_accum", _p), ("lse_accum", _p),
+    ]
+
+
+_ARGP = {
+    "fa_fwd": FaFwdArgs,
+    "fa_bwd_preprocess": FaBwdArgs,
+    "fa_bwd_dq": FaBwdArgs,
+    "fa_bwd_dkdv": FaBwdArgs,
+    "fa_bwd": FaBwdArgs,
+    "fa_kv_append": FaKvcacheArgs,
+    "fa_kv_splitkv": FaKvcacheArgs,
+    "fa_kv_combine": FaKvcacheArgs,
+    "fa_fwd_kvcache": FaKvcacheArgs,
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libfa_mi355x.so once and declare every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built; run flash-attention-turing_amd/build.py")
+    lib = ctypes.CDLL(path)
+    for name, st in _ARGP.items():
+        fn = getattr(lib, name)
+        fn.argtypes = [ctypes.POINTER(st), _p]
+        fn.restype = ctypes.c_int
+    lib.fa_kv_num_splits.argtypes = [ctypes.c_int] * 8
+    lib.fa_kv_num_splits.restype = ctypes.c_int
+    lib.fa_kv_workspace_bytes.argtypes = [ctypes.POINTER(FaKvcacheArgs)]
+    lib.fa_kv_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_error_string.argtypes = [ctypes.c_int]
+    lib.fa_error_string.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def tensor_desc(t, packed: bool = False) -> FaTensor:
+    """[batch][row][head][d] (or packed [total][head][d]) strided view -> FaTensor."""
+    if t is None:
+        return FaTensor(None, 0, 0, 0)
+    if packed:
+        return FaTensor(t.data_ptr(), 0, t.stride(0), t.stride(1))
+    return FaTensor(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(stream=None) -> int:
+    """The raw hipStream_t of a torch stream (current stream by default)."""
+    import torch
+
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+def call(name: str, args, stream=None) -> None:
+    """Invoke entry point ``name``; raise RuntimeError with the library's message on error."""
+    lib = load()
+    rc = getattr(lib, name)(ctypes.byref(args), ctypes.c_void_p(stream_handle(stream)))
+    if rc != FA_OK:
+        raise RuntimeError(f"{name} failed: {lib.fa_error_string(rc).decode()}")
+
+
+def fwd_args(q, k, v, o, lse, softmax_scale: float, causal: bool, cu_seqlens_q=None, cu_seqlens_k=None,
+             max_seqlen_q: int = 0, max_seqlen_k: int = 0) -> FaFwdArgs:
+    packed = cu_seqlens_q is not None
+    a = FaFwdArgs()
+    a.q, a.k, a.v, a.o = (tensor_desc(x, packed) for x in (q, k, v, o))
+    a.lse = lse.data_ptr()
+    a.cu_seqlens_q, a.cu_seqlens_k = ptr(cu_seqlens_q), ptr(cu_seqlens_k)
+    if packed:
+        a.batch = cu_seqlens_q.numel() - 1
+        a.seqlen_q, a.seqlen_k = max_seqlen_q, max_seqlen_k
+        a.nheads, a.nheads_k, a.head_dim = q.shape[1], k.shape[1], q.shape[2]
+        a.lse_seqlen = max_seqlen_q
+    else:
+        a.batch, a.seqlen_q, a.nheads, a.head_dim = q.shape
+        a.seqlen_k, a.nheads_k = k.shape[1], k.shape[2]
+        a.lse_seqlen = q.shape[1]
+    a.softmax_scale = softmax_scale
+    a.causal = int(causal)
+    return a
+
+
+def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, causal: bool, cu_seqlens_q=None,
+             cu_seqlens_k=None, max_seqlen_q: int = 0, max_seqlen_k: int = 0) -> FaBwdArgs:
+    packed = cu_seqlens_q is not None
+    a = FaBwdArgs()
+    a.q, a.k, a.v, a.o, a.dout, a.dq, a.dk, a.dv = (
+        tensor_desc(x, packed) for x in (q, k, v, o, dout, dq, dk, dv)
+    )
+    a.lse, a.dsum = lse.data_ptr(), dsum.data_ptr()
+    a.cu_seqlens_q, a.cu_seqlens_k = ptr(cu_seqlens_q), ptr(cu_seqlens_k)
+    if packed:
+        a.batch = cu_seqlens_q.numel() - 1
+        a.seqlen_q, a.seqlen_k = max_seqlen_q, max_seqlen_k
+        a.nheads, a.nheads_k, a.head_dim = q.shape[1], k.shape[1], q.shape[2]
+        a.lse_seqlen = max_seqlen_q
+    else:
+        a.batch, a.seqlen_q, a.nheads, a.head_dim = q.shape
+        a.seqlen_k, a.nheads_k = k.shape[1], k.shape[2]
+        a.lse_seqlen = q.shape[1]
+    a.softmax_scale = softmax_scale
+    a.causal = int(causal)
+    return a
+
+
+def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: float, causal: bool, num_splits: int,
+                 k_new=None, v_new=None, cache_batch_idx=None, block_table=None, out_accum=None,
+                 lse_accum=None) -> FaKvcacheArgs:
+    a = FaKvcacheArgs()
+    a.q, a.k_cache, a.v_cache, a.o = (tensor_desc(x) for x in (q, k_cache, v_cache, o))
+    a.k_new, a.v_new = tensor_desc(k_new), tensor_desc(v_new)
+    a.lse = lse.data_ptr()
+    a.cache_seqlens, a.cache_batch_idx, a.block_table = ptr(cache_seqlens), ptr(cache_batch_idx), ptr(block_table)
+    a.block_table_stride = block_table.stride(0) if block_table is not None else 0
+    a.batch, a.seqlen_q, a.nheads, a.head_dim = q.shape
+    a.nheads_k = k_cache.shape[2]
+    a.seqlen_new = 0 if k_new is None else k_new.shape[1]
+    a.page_block_size = k_cache.shape[1] if block_table is not None else 0
+    a.num_splits = num_splits
+    a.softmax_scale = softmax_scale
+    a.causal = int(causal)
+    a.out_accum, a.lse_accum = ptr(out_accum), ptr(lse_accum)
+    return a

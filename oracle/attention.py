@@ -183,3 +183,58 @@ def varlen_bwd(
         dq[q0:q1], dk[k0:k1], dv[k0:k1] = g[0][0], g[1][0], g[2][0]
     return dq, dk, dv
 
+
+
+def bwd_fp32_noise(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    dout: torch.Tensor,
+    softmax_scale: float,
+    causal: bool,
+    growth: float = 4.0,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Per-element fp32 rounding-noise scale of (dq, dk, dv), in float32.
+
+    First-order error model of any fp32 evaluation of the backward (the
+    reference's MMA dP and warp-shuffle D, flash_bwd_kernel.h:385-436 and
+    preprocess.h:74-94, as much as a HIP kernel), with eps = fp32 epsilon:
+      * P = exp(scale*S - LSE): relative error rho_ij = eps * (|scale| (|Q||K|^T)_ij + |LSE_i| + 1);
+      * dP - D: absolute error eps * A_ij, A_ij = (|dO||V|^T)_ij + sum_d |O_id dO_id|;
+      * dS = P (dP - D): P rho |dP - D| + eps P A;
+      * dV = P^T dO, dQ = scale dS K, dK = scale dS^T Q: the above pushed
+        through absolute values, plus eps times the sum of |terms|;
+    times ``growth`` for accumulation-order effects.  Where dP == D in real
+    arithmetic (a row with one visible key, O = v) dS is pure noise of this
+    size, which the twin's fp16 rounding points cannot show.
+    """
+    eps = torch.finfo(torch.float32).eps
+    dt = torch.float64
+    b, sq, h, d = q.shape
+    sk, hk = k.shape[1], k.shape[2]
+    groups = h // hk
+    sc = abs(softmax_scale)
+    qa = q.to(dt).permute(0, 2, 1, 3)
+    ka = _expand_kv(k.to(dt), groups).permute(0, 2, 1, 3)
+    va = _expand_kv(v.to(dt), groups).permute(0, 2, 1, 3)
+    oa = out.to(dt).permute(0, 2, 1, 3)
+    doa = dout.to(dt).permute(0, 2, 1, 3)
+    l = lse.to(dt)[..., None]
+    p = torch.exp(torch.matmul(qa, ka.transpose(-1, -2).contiguous()) * softmax_scale - l)
+    if causal:
+        p = p.masked_fill(~causal_keep(sq, sk), 0.0)
+    rho = eps * (sc * torch.matmul(qa.abs(), ka.abs().transpose(-1, -2).contiguous()) + l.abs() + 1.0)
+    dp_minus_d = torch.matmul(doa, va.transpose(-1, -2).contiguous()) - (oa * doa).sum(-1, keepdim=True)
+    amag = torch.matmul(doa.abs(), va.abs().transpose(-1, -2).contiguous()) + (oa * doa).abs().sum(-1, keepdim=True)
+    ds_abs = p * dp_minus_d.abs()
+    ds_err = p * rho * dp_minus_d.abs() + eps * p * amag
+    dq = sc * (torch.matmul(ds_err, ka.abs()) + eps * torch.matmul(ds_abs, ka.abs()))
+    dk = sc * (torch.matmul(ds_err.transpose(-1, -2).contiguous(), qa.abs())
+               + eps * torch.matmul(ds_abs.transpose(-1, -2).contiguous(), qa.abs()))
+    pt = (p * (rho + eps)).transpose(-1, -2).contiguous()
+    dv = torch.matmul(pt, doa.abs())
+    dk = dk.reshape(b, hk, groups, sk, d).sum(dim=2)
+    dv = dv.reshape(b, hk, groups, sk, d).sum(dim=2)
+    return tuple((growth * x).permute(0, 2, 1, 3).contiguous().float() for x in (dq, dk, dv))

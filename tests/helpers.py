@@ -35,11 +35,21 @@ def bound_2x(err_ref: float) -> float:
     return 2.0 * err_ref + ABS_FLOOR
 
 
-def assert_2x(name: str, got: torch.Tensor, oracle: torch.Tensor, twin: torch.Tensor) -> Dict[str, float]:
+def assert_2x(name: str, got: torch.Tensor, oracle: torch.Tensor, twin: torch.Tensor, noise=None) -> Dict[str, float]:
+    """max|got - oracle| <= 2 x max|twin - oracle| + ABS_FLOOR, elementwise
+    widened by ``noise`` (the fp32 accumulation-noise scale of each element,
+    oracle.attention.bwd_fp32_noise) where the twin cannot show that noise."""
     e_got = max_abs(got, oracle)
     e_ref = max_abs(twin, oracle)
     assert math.isfinite(e_got), f"{name}: non-finite output"
-    assert e_got <= bound_2x(e_ref), f"{name}: max-abs {e_got:.3e} > 2 x reference-twin error {e_ref:.3e}"
+    if noise is None:
+        assert e_got <= bound_2x(e_ref), f"{name}: max-abs {e_got:.3e} > 2 x reference-twin error {e_ref:.3e}"
+    else:
+        diff = (got.float().cpu() - oracle.float().cpu()).abs()
+        excess = (diff - bound_2x(e_ref) - noise.float().cpu()).max().item() if diff.numel() else 0.0
+        assert excess <= 0.0, (
+            f"{name}: max-abs {e_got:.3e} exceeds 2 x reference-twin error {e_ref:.3e} + fp32 noise by {excess:.3e}"
+        )
     return {"err": e_got, "err_ref": e_ref}
 
 

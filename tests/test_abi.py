@@ -55,3 +55,33 @@ def test_num_splits_heuristic(lib):
     s = f(0, 32768, 128, 1, 4, 32, 8, 256)
     assert 1 < s <= 64
     assert f(0, 1 << 20, 128, 1, 1, 8, 1, 256) <= 128
+
+
+def test_ctypes_structs_match_the_c_layout(tmp_path):
+    """fa_capi's ctypes structs have the size and field offsets gcc gives the
+    structs of include/fa_mi355x.h (a mismatch would pass garbage to kernels)."""
+    import shutil
+    import subprocess
+
+    import fa_capi
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    structs = {"fa_tensor": fa_capi.FaTensor, "fa_fwd_args": fa_capi.FaFwdArgs, "fa_bwd_args": fa_capi.FaBwdArgs,
+               "fa_kvcache_args": fa_capi.FaKvcacheArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "fa_mi355x.h"', "int main(void) {"]
+    for cname, st in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in st._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    for line in filter(None, got):
+        cname, field, value = line.split()
+        st = structs[cname]
+        expect = ctypes.sizeof(st) if field == "size" else getattr(st, field).offset
+        assert int(value) == expect, f"{cname}.{field}: C {value} vs ctypes {expect}"

@@ -10,7 +10,7 @@ import torch
 
 import flash_attention_interface as fai
 from helpers import assert_2x, randn16
-from oracle.attention import attention_bwd, attention_fwd
+from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise
 from oracle.twin import bwd_twin, fwd_twin
 
 SEQLENS = [(1, 1), (37, 1), (63, 65), (128, 128), (127, 129), (257, 190), (190, 257), (512, 512), (700, 1025)]
@@ -28,7 +28,8 @@ def _oracles(q, k, v, do, s, causal):
     grads_ref = attention_bwd(q, k, v, o_ref, l_ref, do, s, causal)
     o_tw, l_tw = fwd_twin(q, k, v, s, causal)
     grads_tw = bwd_twin(q, k, v, o_tw, l_tw, do, s, causal)
-    return grads_ref, grads_tw
+    noise = bwd_fp32_noise(q, k, v, o_ref, l_ref, do, s, causal)
+    return grads_ref, grads_tw, noise
 
 
 @pytest.mark.gpu
@@ -45,11 +46,11 @@ def test_bwd_parity(device, hd, causal, sq, sk, heads, batch, scale):
     out = fai.flash_attn_func(qd, kd, vd, softmax_scale=scale, causal=causal)
     out.backward(do.to(device))
     torch.cuda.synchronize()
-    (dq_r, dk_r, dv_r), (dq_t, dk_t, dv_t) = _oracles(q, k, v, do, s, causal)
+    (dq_r, dk_r, dv_r), (dq_t, dk_t, dv_t), (nq, nk, nv) = _oracles(q, k, v, do, s, causal)
     assert kd.grad.shape == k.shape and vd.grad.shape == v.shape
-    assert_2x("dq", qd.grad, dq_r, dq_t)
-    assert_2x("dk", kd.grad, dk_r, dk_t)
-    assert_2x("dv", vd.grad, dv_r, dv_t)
+    assert_2x("dq", qd.grad, dq_r, dq_t, nq)
+    assert_2x("dk", kd.grad, dk_r, dk_t, nk)
+    assert_2x("dv", vd.grad, dv_r, dv_t, nv)
 
 
 @pytest.mark.gpu

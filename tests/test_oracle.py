@@ -19,7 +19,7 @@ import torch
 
 from oracle import kvcache as okv
 from oracle import twin
-from oracle.attention import attention_bwd, attention_fwd, causal_keep, varlen_bwd, varlen_fwd
+from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise, causal_keep, varlen_bwd, varlen_fwd
 
 D64 = torch.float64
 
@@ -154,6 +154,25 @@ def test_bwd_finite_differences():
             args_p[gi], args_m[gi] = tp, tm
             fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
             assert abs(fd - grads[gi][idx].item()) < 1e-7
+
+
+@pytest.mark.parametrize("sq,sk,h,hk,causal", [(37, 1, 6, 1, False), (50, 40, 4, 2, True)])
+def test_bwd_noise_floor_covers_fp32_and_stays_small(sq, sk, h, hk, causal):
+    """The fp32 noise scale covers what fp32 arithmetic in another summation
+    order does (here: the fp32 closed form vs float64), including the single
+    key case where dP == D and dK is pure rounding noise, and stays far below
+    the gradients' own size, so a dropped term or wrong index cannot hide in it."""
+    g = torch.Generator().manual_seed(23)
+    q, k, v, do = (torch.randn(s, generator=g).half() for s in ((2, sq, h, 128), (2, sk, hk, 128), (2, sk, hk, 128), (2, sq, h, 128)))
+    o64, l64 = attention_fwd(q, k, v, 0.3, causal, dtype=D64)
+    g64 = attention_bwd(q, k, v, o64, l64, do, 0.3, causal, dtype=D64)
+    g32 = attention_bwd(q, k, v, o64.float(), l64.float(), do, 0.3, causal)
+    noise = bwd_fp32_noise(q, k, v, o64, l64, do, 0.3, causal)
+    for a, b, n in zip(g32, g64, noise):
+        assert torch.all((a.double() - b).abs() <= n.double())
+    if sk > 1:
+        for b, n in zip(g64, noise):
+            assert n.max().item() < 1e-3 * b.abs().max().item()
 
 
 def test_varlen_equals_dense_per_sequence():

@@ -7,7 +7,7 @@ import torch
 
 import flash_attention_interface as fai
 from helpers import assert_2x, assert_lse, cu_from_lengths, randn16
-from oracle.attention import attention_bwd, attention_fwd
+from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise
 from oracle.twin import bwd_twin, fwd_twin
 
 CASES = [
@@ -44,6 +44,7 @@ def test_varlen_parity(device, lens_q, lens_k, h, hk, hd, causal):
     o_tw = torch.zeros(q.shape, dtype=torch.float16)
     g_ref = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
     g_tw = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
+    g_noise = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
     lse_ref = torch.zeros((len(lens_q), h, mq))
     for b in range(len(lens_q)):
         q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
@@ -53,12 +54,13 @@ def test_varlen_parity(device, lens_q, lens_k, h, hk, hd, causal):
         o_ref[q0:q1], o_tw[q0:q1], lse_ref[b, :, : q1 - q0] = ob[0], otb[0], lb[0]
         gr = attention_bwd(qb, kb, vb, ob, lb, dob, s, causal)
         gt = bwd_twin(qb, kb, vb, otb, ltb, dob, s, causal)
+        gn = bwd_fp32_noise(qb, kb, vb, ob, lb, dob, s, causal)
         for i, (lo, hi) in enumerate([(q0, q1), (k0, k1), (k0, k1)]):
-            g_ref[i][lo:hi], g_tw[i][lo:hi] = gr[i][0], gt[i][0].float()
+            g_ref[i][lo:hi], g_tw[i][lo:hi], g_noise[i][lo:hi] = gr[i][0], gt[i][0].float(), gn[i][0]
     assert_2x("out", out, o_ref, o_tw)
     assert_lse(lse, lse_ref)  # includes the zero padding past each length
-    for name, got, r, t in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref, g_tw):
-        assert_2x(name, got, r, t)
+    for name, got, r, t, n in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref, g_tw, g_noise):
+        assert_2x(name, got, r, t, n)
 
 
 @pytest.mark.gpu
