@@ -38,6 +38,18 @@ for _p in (PKG, REPO):
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 
+# HBM bytes per launch (read + write) of the headline-shape kernels, from
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only train
+# --no-8k` / `--only decode`, scaled by the counters' reading of a 1 GiB copy
+# (FETCH x 2.0, WRITE x 1.0); summary in profiles/hbm_bytes_pmc_c2_c4.md.
+# Re-measured whenever a kernel changes; None where not measured.
+PMC_TRAFFIC_BYTES = {
+    "fwd": 6.694e8 + 6.82e7,
+    "bwd_dq": 7.445e8 + 6.72e7,
+    "bwd_dkdv": 7.406e8 + 1.827e8,
+    "kv_splitkv": 4.699e9 + 8.5e6,
+}
+
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -233,7 +245,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "train", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "train", "decode", "copy"], default="all",
+                    help="copy: a plain 1 GiB device copy, the calibration kernel for HBM byte counters")
+    ap.add_argument("--no-8k", action="store_true", help="omit the seqlen 8192 point")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (collectives, sharding) "
@@ -250,6 +264,16 @@ def main():
     result = {}
 
     b, s, h, d = 4, 4096, 16, 128
+    if args.only == "copy":
+        n = 1 << 29  # fp16 elements: 1 GiB read + 1 GiB written per copy
+        src = torch.randn(n, device=device, dtype=torch.float16)
+        dst = torch.empty_like(src)
+        ms, per = Timed([("copy", lambda: dst.copy_(src))]).run(args.steps, args.warmup)
+        gbs = 2 * n * 2 / (per["copy"] * 1e-3) / 1e9
+        print(json.dumps({"metric": "device copy GB/s (HBM counter calibration)", "value": round(gbs, 1),
+                          "unit": "GB/s", "bytes_read": 2 * n, "bytes_written": 2 * n,
+                          "ms": round(per["copy"], 4)}), flush=True)
+        return
     if args.only in ("all", "train"):
         log("headline: causal fwd+bwd b4 s4096 h16 d128 (seed 1)")
         launches, tensors = train_step_setup(b, s, h, d, 1, device)
@@ -265,7 +289,8 @@ def main():
             unit="TFLOPS",
             ms_per_step=round(ms_step, 4),
             roofline={"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP16_TFLOPS,
-                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None},
+                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                      "traffic": PMC_TRAFFIC_BYTES.get(dom)},
             train_s4096=rep,
         )
         log(f"s4096: {rep}")
@@ -275,14 +300,15 @@ def main():
         del launches, tensors
         torch.cuda.empty_cache()
 
-        log("north-star point: causal fwd+bwd b4 s8192 h16 d128 (seed 5)")
-        launches, tensors = train_step_setup(b, 8192, h, d, 5, device)
-        ms8, per8 = Timed(launches).run(max(3, args.steps // 2), max(1, args.warmup // 2))
-        rep8, _, _ = train_report(b, 8192, h, d, ms8, per8)
-        result["train_s8192"] = rep8
-        log(f"s8192: {rep8}")
-        del launches, tensors
-        torch.cuda.empty_cache()
+        if not args.no_8k:
+            log("north-star point: causal fwd+bwd b4 s8192 h16 d128 (seed 5)")
+            launches, tensors = train_step_setup(b, 8192, h, d, 5, device)
+            ms8, per8 = Timed(launches).run(max(3, args.steps // 2), max(1, args.warmup // 2))
+            rep8, _, _ = train_report(b, 8192, h, d, ms8, per8)
+            result["train_s8192"] = rep8
+            log(f"s8192: {rep8}")
+            del launches, tensors
+            torch.cuda.empty_cache()
 
     if args.only in ("all", "decode"):
         log("decode c4: paged split-KV with append (seed 3)")
@@ -304,7 +330,8 @@ def main():
                           ms_per_step=info["ms_per_call"],
                           roofline={"kernel": "kv_splitkv", "bound": "hbm", "achieved": info["gbs_splitkv"],
                                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                    "frac": round(info["gbs_splitkv"] / PEAK_HBM_GBS, 4), "traffic": None})
+                                    "frac": round(info["gbs_splitkv"] / PEAK_HBM_GBS, 4),
+                                    "traffic": PMC_TRAFFIC_BYTES.get("kv_splitkv")})
 
     line = {
         "metric": result.pop("metric"),
