@@ -107,6 +107,44 @@ __device__ __forceinline__ void tr_store4(char *base, int k0, int x0, const u32x
 }
 
 // ---------------------------------------------------------------------------
+// gfx950 direct global -> LDS copies and LDS transpose reads.
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
+
+// global_load_lds_dwordx4: lane l's 16 bytes at `g` land at lds_base + 16*l.
+// lds_base must be the same for the whole wave.  Completion is tracked by
+// vmcnt only: wait with wait_vmem() before a barrier that publishes the tile.
+__device__ __forceinline__ void g2l16(const void *g, char *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds_base, 16, 0, 0);
+}
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ds_read_b64_tr_b16.  Within each group of 16 lanes, lane i receives element
+// j (j = 0..3) = the 16-bit word at (address of group lane 4*j + i/4) + 2*(i%4)
+// bytes.  Pointing group lane s = 4*j + q at row r0 + j, column c0 + 4*q of a
+// row-major fp16 tile therefore hands lane i the 4 words (r0 + j, c0 + i):
+// a 4-row x 16-column block transposed across the 16 lanes.
+__device__ __forceinline__ f16x4 lds_tr4(const char *base, int off) {
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + off)));
+}
+
+// Natural [rows][KCH chunks] tiles read as MFMA A operands (rows sigma(0..31)
+// at one chunk): chunk c of row r sits at chunk c ^ swz_rows(r).
+template <int KCH>
+__device__ __forceinline__ int swz_rows(int row) {
+    return sigma(row) & (KCH - 1);
+}
+// Natural tiles read with lds_tr4 (per instruction 8 rows x 64 bytes, 4 rows x
+// 32 bytes per 16 lanes): conflict-free placement for 16- and 32-lane phases.
+template <int KCH>
+__device__ __forceinline__ int swz_tr(int row) {
+    return KCH == 16 ? (((row & 1) ? 4 : 0) ^ ((row & 2) ? 10 : 0)) : (((row & 1) ? 2 : 0) ^ ((row & 2) ? 4 : 0));
+}
+
+// ---------------------------------------------------------------------------
 // Global memory.
 
 __device__ __forceinline__ u32x4 ldg16(const f16 *p) { return *reinterpret_cast<const u32x4 *>(p); }

@@ -12,28 +12,30 @@
 // wave owns 32 queries.  The wave computes S^T = K Q^T (keys on the MFMA M
 // dimension) so each lane holds one query column and 32 keys of a 64-key
 // block: the row max needs one cross-half exchange and the row sum none.
-// Q^T stays in registers as the B operand; K (natural) and V (transposed)
-// tiles are double-buffered in LDS with one barrier per block; P^T feeds the
-// O^T += V^T P^T MFMAs directly from the accumulators (see fa_common.h).
+// Q^T stays in registers as the B operand.  K and V tiles go from HBM
+// straight into LDS with global_load_lds (no register staging), two stages,
+// the next block's copy in flight while the current block is computed; V is
+// kept in its natural layout and read transposed with ds_read_b64_tr_b16.
+// P^T feeds the O^T += V^T P^T MFMAs directly from the accumulators (see
+// fa_common.h).  Two workgroups share a CU (64 KB LDS each at head_dim 128),
+// so one wave's softmax overlaps the other's MFMAs on each SIMD.
 #include "fa_common.h"
 
 namespace fa {
 
 template <int HD>
 struct FwdCfg {
-    static constexpr int BM = 128;               // queries per workgroup
-    static constexpr int BN = 64;                // keys per block
-    static constexpr int NT = 256;               // threads
-    static constexpr int KCH = HD / 8;           // 16-byte chunks per row
-    static constexpr int K_BYTES = BN * HD * 2;  // natural K tile
-    static constexpr int V_BYTES = HD * BN * 2;  // transposed V tile
-    static constexpr int STAGE = K_BYTES + V_BYTES;
-    static constexpr int K_LD = BN * KCH / NT;   // K chunks per thread
-    static constexpr int V_UNITS = (BN / 4) * KCH;
+    static constexpr int BM = 128;                // queries per workgroup
+    static constexpr int BN = 64;                 // keys per block
+    static constexpr int NT = 256;                // threads
+    static constexpr int KCH = HD / 8;            // 16-byte chunks per row
+    static constexpr int TILE = BN * HD * 2;      // one K or V tile
+    static constexpr int STAGE = 2 * TILE;        // K tile, then V tile
+    static constexpr int CPT = BN * KCH / NT;     // chunks per thread per tile
 };
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
+__global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
     using C = FwdCfg<HD>;
     constexpr int BM = C::BM, BN = C::BN, NT = C::NT, KCH = C::KCH;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
@@ -93,48 +95,36 @@ __global__ __launch_bounds__(256) void fwd_kernel(const fa_fwd_args a, const int
     float m_t = -INFINITY;  // running max of scale*log2(e)*S for this lane's query
     float l_p = 0.f;        // partial row sum over this lane half's keys
 
-    u32x4 kreg[C::K_LD];
-    u32x4 vreg[4];
-    const bool v_thread = tid < C::V_UNITS;
-    const int vm = tid % (BN / 4), vc = tid / (BN / 4);
-
-    auto load_kv = [&](int nb) {
+    // Copy of key block nb into stage st: chunk p = (i*4 + wave)*64 + lane of
+    // each tile holds chunk (p % KCH) ^ swz of row p / KCH.  Rows past the
+    // sequence re-read its last key (finite values; masked below).
+    auto issue = [&](int nb, int st) {
+        char *ks = smem + st * C::STAGE;
+        char *vs = ks + C::TILE;
         const int n0 = nb * BN;
 #pragma unroll
-        for (int i = 0; i < C::K_LD; ++i) {
-            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
-            const int key = n0 + row;
-            kreg[i] = key < sk ? ldg16(kp + int64_t(key) * krs + 8 * c) : zero_u4();
+        for (int i = 0; i < C::CPT; ++i) {
+            const int base = (i * 4 + wave) * 64;
+            const int p = base + lane, row = p / KCH, cs = p % KCH;
+            const int64_t key = min(n0 + row, sk - 1);
+            g2l16(kp + key * krs + 8 * (cs ^ swz_rows<KCH>(row)), ks + base * 16);
+            g2l16(vp + key * vrs + 8 * (cs ^ swz_tr<KCH>(row)), vs + base * 16);
         }
-        if (v_thread) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = n0 + 4 * vm + r;
-                vreg[r] = key < sk ? ldg16(vp + int64_t(key) * vrs + 8 * vc) : zero_u4();
-            }
-        }
-    };
-    auto store_kv = [&](int buf) {
-        char *ks = smem + buf * C::STAGE;
-        char *vs = ks + C::K_BYTES;
-#pragma unroll
-        for (int i = 0; i < C::K_LD; ++i) {
-            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
-            lds_st16(ks, nat_off<HD>(row, c), kreg[i]);
-        }
-        if (v_thread) tr_store4<BN>(vs, 4 * vm, 8 * vc, vreg[0], vreg[1], vreg[2], vreg[3]);
     };
 
-    if (n_blocks > 0) {
-        load_kv(0);
-        store_kv(0);
-    }
-    __syncthreads();
+    // Per-lane parts of the transposed V reads (see lds_tr4): group lane
+    // s = 4*j + q points at row 8*hh + j, columns 16*db + 4*q of a 32-column slab.
+    const int tr_j = (lane & 15) >> 2, tr_q = lane & 3, tr_db = (lane >> 4) & 1;
+    const int tr_row = 8 * hh + tr_j;
+
+    if (n_blocks > 0) issue(0, 0);
 
     const int q_lo = m0 + wave * 32;
     for (int nb = 0; nb < n_blocks; ++nb) {
         const int buf = nb & 1;
-        if (nb + 1 < n_blocks) load_kv(nb + 1);
+        wait_vmem();
+        __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
+        if (nb + 1 < n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
 
         bool active = true;
@@ -143,76 +133,82 @@ __global__ __launch_bounds__(256) void fwd_kernel(const fa_fwd_args a, const int
             if (n0 > q_lo + 31 + causal_off) active = false;
             if (n0 + BN - 1 > q_lo + causal_off) need_mask = true;
         }
-        if (active) {
-            const char *ks = smem + buf * C::STAGE;
-            const char *vs = ks + C::K_BYTES;
-            f32x16 s[2];
+        if (!active) continue;
+        const char *ks = smem + buf * C::STAGE;
+        const char *vs = ks + C::TILE;
+        f32x16 s[2];
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                s[kt] = zero16();
-                const int row = kt * 32 + sigma(col);
+        for (int kt = 0; kt < 2; ++kt) {
+            s[kt] = zero16();
+            const int row = kt * 32 + sigma(col);
+            const int rbase = row * (HD * 2), sw = swz_rows<KCH>(row);
 #pragma unroll
-                for (int g = 0; g < HD / 16; ++g) s[kt] = mfma32(lds_ld16(ks, nat_off<HD>(row, 2 * g + hh)), qB[g], s[kt]);
-            }
+            for (int g = 0; g < HD / 16; ++g)
+                s[kt] = mfma32(lds_ld16(ks, rbase + (((2 * g + hh) ^ sw) << 4)), qB[g], s[kt]);
+        }
 
-            float mx = -INFINITY;
-            if (need_mask) {
-                const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (n0 + kt * 32 + acc_lrow(r, hh) > lim) s[kt][r] = -INFINITY;
-            }
+        float mx = -INFINITY;
+        if (need_mask) {
+            const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
-            const float m_new = fmaxf(m_t, mx_t);
-            const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            float rs = 0.f;
-            if (need_mask) {
+                for (int r = 0; r < 16; ++r)
+                    if (n0 + kt * 32 + acc_lrow(r, hh) > lim) s[kt][r] = -INFINITY;
+        }
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float x = s[kt][r];
-                        const float p = x == -INFINITY ? 0.f : exp2_fast(fmaf(x, cscale, -m_use));
-                        s[kt][r] = p;
-                        rs += p;
-                    }
-            } else {
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
+        const float m_new = fmaxf(m_t, mx_t);
+        const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        float rs = 0.f;
+        if (need_mask) {
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float p = exp2_fast(fmaf(s[kt][r], cscale, -m_use));
-                        s[kt][r] = p;
-                        rs += p;
-                    }
-            }
-            l_p = l_p * alpha + rs;
-            m_t = m_new;
+                for (int r = 0; r < 16; ++r) {
+                    const float x = s[kt][r];
+                    const float p = x == -INFINITY ? 0.f : exp2_fast(fmaf(x, cscale, -m_use));
+                    s[kt][r] = p;
+                    rs += p;
+                }
+        } else {
 #pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt)
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+                for (int r = 0; r < 16; ++r) {
+                    const float p = exp2_fast(fmaf(s[kt][r], cscale, -m_use));
+                    s[kt][r] = p;
+                    rs += p;
+                }
+        }
+        l_p = l_p * alpha + rs;
+        m_t = m_new;
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
 
-            f16x8 pB[4];
+        f16x8 pB[4];
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg) pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+        for (int gg = 0; gg < 4; ++gg) pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
 #pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt) {
-                const int d = dt * 32 + col;
+        for (int dt = 0; dt < HD / 32; ++dt) {
+            const int c0 = 4 * dt + 2 * tr_db + (tr_q >> 1);
+            const int byte = (tr_q & 1) * 8;
 #pragma unroll
-                for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(lds_ld16(vs, tr_off<BN>(d, 2 * gg + hh)), pB[gg], o[dt]);
+            for (int gg = 0; gg < 4; ++gg) {
+                const int r0 = 16 * gg + tr_row, r1 = r0 + 4;
+                const f16x4 lo = lds_tr4(vs, r0 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r0)) << 4) + byte);
+                const f16x4 hi = lds_tr4(vs, r1 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r1)) << 4) + byte);
+                const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[dt] = mfma32(va, pB[gg], o[dt]);
             }
         }
-        if (nb + 1 < n_blocks) store_kv(buf ^ 1);
-        __syncthreads();
     }
 
     // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
