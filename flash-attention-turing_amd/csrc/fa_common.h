@@ -114,13 +114,35 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
 
 // global_load_lds_dwordx4: lane l's 16 bytes at `g` land at lds_base + 16*l.
-// lds_base must be the same for the whole wave.  Completion is tracked by
-// vmcnt only: wait with wait_vmem() before a barrier that publishes the tile.
+// lds_base must be the same for the whole wave.  Issued from inline assembly
+// (M0 saved and restored around it) so that the compiler does not treat the
+// copy as a pending write to all of LDS: its automatic waits would otherwise
+// stall every transposed LDS read until the prefetched tile has landed.  The
+// compiler therefore does not count these copies either: wait for them
+// explicitly (wait_vmem / wait_vmem_n) before a barrier that publishes the
+// tile, and issue no other vector-memory loads while copies are in flight
+// (the compiler's own waits for those would then also cover the copies).
 __device__ __forceinline__ void g2l16(const void *g, char *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds_base, 16, 0, 0);
+    const uint32_t l =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds_base);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(l)
+        : "memory");
 }
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N), N < 64.
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
 // ds_read_b64_tr_b16.  Within each group of 16 lanes, lane i receives element
 // j (j = 0..3) = the 16-bit word at (address of group lane 4*j + i/4) + 2*(i%4)

@@ -16,13 +16,16 @@
 // K/V byte of the split is read once.  The keys of the split are walked in
 // 32-key tiles aligned to absolute positions (a tile never straddles a page:
 // pages are multiples of 256 tokens), tile t going to wave t % 4.  Each wave
-// keeps its own online softmax state and stages its tile through a private
-// LDS region (K natural, V transposed), so the main loop has no workgroup
-// barrier; the next tile's loads are in flight while the current tile is
-// computed.  The four waves merge their partial states through LDS at the end.
-// Paged, remapped and contiguous caches take the same tile order and the same
+// streams its tiles through a private two-stage LDS ring with direct
+// global -> LDS copies (global_load_lds): while one tile is computed the next
+// one is in flight, with no register staging and no workgroup barrier in the
+// loop.  K stays natural (MFMA A operand rows), V natural and read transposed
+// with ds_read_b64_tr_b16.  Each wave keeps its own online softmax state; the
+// four waves merge their partial states through LDS at the end.  Paged,
+// remapped and contiguous caches take the same tile order and the same
 // arithmetic, so their results are bit-identical for the same logical cache.
 #include <algorithm>
+#include <type_traits>
 
 #include "fa_common.h"
 
@@ -77,12 +80,12 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a)
 template <int HD>
 struct KvCfg {
     static constexpr int KCH = HD / 8;
-    static constexpr int KN = kTile * HD * 2;  // natural K tile (per wave)
-    static constexpr int VT = HD * kTile * 2;  // transposed V tile (per wave)
-    static constexpr int WAVE_LDS = KN + VT;   // also holds HD x 32 fp32 at the merge (same size)
-    static constexpr int K_LD = kTile * KCH / 64;        // K chunks per lane
-    static constexpr int V_UNITS = (kTile / 4) * KCH;    // 4-row units per tile
-    static constexpr int V_LD = V_UNITS / 64;            // units per lane
+    static constexpr int TILE = kTile * HD * 2;         // one K or V tile, natural layout
+    static constexpr int STAGE = 2 * TILE;              // K tile, then V tile
+    static constexpr int NST = 2;                       // ring stages per wave
+    static constexpr int WAVE_LDS = NST * STAGE;        // also holds HD x 32 fp32 at the merge
+    static constexpr int CPW = kTile * KCH / 64;        // DMA instructions per lane per tile (K or V)
+    static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
 };
 
 template <int HD>
@@ -90,8 +93,10 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
     using C = KvCfg<HD>;
     constexpr int KCH = C::KCH;
     __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
+    __shared__ int pages[C::MAX_PAGES];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int col = lane & 31, hh = lane >> 5;
     const int split = blockIdx.y;
     int rest = blockIdx.x;
@@ -133,55 +138,81 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
     for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
     float m_t = -INFINITY, l_p = 0.f;
 
-    char *ks = smem + wave * C::WAVE_LDS;
-    char *vs = ks + C::KN;
     const int t_first = s0 / kTile;
     const int t_last = s1 > s0 ? (s1 - 1) / kTile : t_first - 1;
+    const int my_first = t_first + wave;
+    const int n_my = my_first <= t_last ? (t_last - my_first) / kKvWaves + 1 : 0;
 
-    u32x4 kreg[C::K_LD], vreg[4 * C::V_LD];
-    auto load = [&](int t) {
+    // Page ids of the split, staged in LDS so the ring never waits on a table read.
+    const int page = a.page_block_size;
+    const int pg_first = a.block_table ? (t_first * kTile) / page : 0;
+    const int n_pages = a.block_table && s1 > s0 ? (t_last * kTile) / page - pg_first + 1 : 0;
+    const bool pages_in_lds = n_pages <= C::MAX_PAGES;
+    if (a.block_table && pages_in_lds) {
+        const int32_t *bt = a.block_table + int64_t(b) * a.block_table_stride + pg_first;
+        for (int i = tid; i < n_pages; i += kKvThreads) pages[i] = bt[i];
+    }
+    __syncthreads();
+
+    const int64_t krs = a.k_cache.row_stride, vrs = a.v_cache.row_stride;
+    const int tr_j = (lane & 15) >> 2, tr_q = lane & 3, tr_db = (lane >> 4) & 1;
+    const int tr_row = 8 * hh + tr_j;
+
+    // The tile loop, instantiated twice: with the split's page ids in LDS (and
+    // no other vector-memory load while copies are in flight), and a fallback
+    // that reads the block table per tile for splits spanning more pages.
+    auto run = [&](auto lds_pages_tag) {
+    constexpr bool LDS_PAGES = decltype(lds_pages_tag)::value;
+    // Copy tile t into ring stage st of this wave.  Rows past L re-read key L - 1
+    // of the same tile (finite values; masked below).
+    auto issue = [&](int t, int st) {
         const int p0 = t * kTile;
-        const f16 *kb = kv_row_ptr(a.k_cache, a, b, cache_row, hk, p0);
-        const f16 *vb = kv_row_ptr(a.v_cache, a, b, cache_row, hk, p0);
-        const int64_t krs = a.k_cache.row_stride, vrs = a.v_cache.row_stride;
-#pragma unroll
-        for (int i = 0; i < C::K_LD; ++i) {
-            const int idx = lane + 64 * i, r = idx / KCH, c = idx % KCH;
-            kreg[i] = p0 + r < L ? ldg16(kb + int64_t(r) * krs + 8 * c) : zero_u4();
+        int64_t koff, voff;
+        if (a.block_table) {
+            const int pi = p0 / page;
+            int blk;
+            if constexpr (LDS_PAGES)
+                blk = pages[pi - pg_first];
+            else
+                blk = a.block_table[int64_t(b) * a.block_table_stride + pi];
+            const int in_page = p0 - pi * page;
+            koff = int64_t(blk) * a.k_cache.batch_stride + int64_t(in_page) * krs;
+            voff = int64_t(blk) * a.v_cache.batch_stride + int64_t(in_page) * vrs;
+        } else {
+            koff = int64_t(cache_row) * a.k_cache.batch_stride + int64_t(p0) * krs;
+            voff = int64_t(cache_row) * a.v_cache.batch_stride + int64_t(p0) * vrs;
         }
+        const f16 *kb = (const f16 *)a.k_cache.ptr + koff + int64_t(hk) * a.k_cache.head_stride;
+        const f16 *vb = (const f16 *)a.v_cache.ptr + voff + int64_t(hk) * a.v_cache.head_stride;
+        char *ks = smem + (wave * C::NST + st) * C::STAGE;
+        char *vs = ks + C::TILE;
+        const int rmax = L - 1 - p0;
 #pragma unroll
-        for (int i = 0; i < C::V_LD; ++i) {
-            const int u = lane + 64 * i, m = u % (kTile / 4), c = u / (kTile / 4);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                vreg[4 * i + r] = p0 + 4 * m + r < L ? ldg16(vb + int64_t(4 * m + r) * vrs + 8 * c) : zero_u4();
+        for (int i = 0; i < C::CPW; ++i) {
+            const int p = i * 64 + lane, r = p / KCH, cs = p % KCH;
+            const int rr = min(r, rmax);
+            g2l16(kb + int64_t(rr) * krs + 8 * (cs ^ swz_rows<KCH>(r)), ks + i * 1024);
+            g2l16(vb + int64_t(rr) * vrs + 8 * (cs ^ swz_tr<KCH>(r)), vs + i * 1024);
         }
     };
-    auto store = [&]() {
-#pragma unroll
-        for (int i = 0; i < C::K_LD; ++i) {
-            const int idx = lane + 64 * i, r = idx / KCH, c = idx % KCH;
-            lds_st16(ks, nat_off<HD>(r, c), kreg[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < C::V_LD; ++i) {
-            const int u = lane + 64 * i, m = u % (kTile / 4), c = u / (kTile / 4);
-            tr_store4<kTile>(vs, 4 * m, 8 * c, vreg[4 * i], vreg[4 * i + 1], vreg[4 * i + 2], vreg[4 * i + 3]);
-        }
-    };
 
-    int t = t_first + wave;
-    if (t <= t_last) load(t);
-    for (; t <= t_last; t += kKvWaves) {
-        store();
-        __builtin_amdgcn_wave_barrier();
-        if (t + kKvWaves <= t_last) load(t + kKvWaves);
-        const int p0 = t * kTile;
+    if (n_my > 0) issue(my_first, 0);
+    if (n_my > 1) issue(my_first + kKvWaves, 1);
+    for (int k = 0; k < n_my; ++k) {
+        const int st = k & 1;
+        if (k + 1 < n_my)
+            wait_vmem_n<2 * C::CPW>();  // the newer tile may stay in flight
+        else
+            wait_vmem();
+        const char *ks = smem + (wave * C::NST + st) * C::STAGE;
+        const char *vs = ks + C::TILE;
+        const int p0 = (my_first + k * kKvWaves) * kTile;
         f32x16 s = zero16();
         {
             const int r = sigma(col);
+            const int rbase = r * (HD * 2), sw = swz_rows<KCH>(r);
 #pragma unroll
-            for (int g = 0; g < HD / 16; ++g) s = mfma32(lds_ld16(ks, nat_off<HD>(r, 2 * g + hh)), qB[g], s);
+            for (int g = 0; g < HD / 16; ++g) s = mfma32(lds_ld16(ks, rbase + (((2 * g + hh) ^ sw) << 4)), qB[g], s);
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -219,22 +250,33 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
         for (int dt = 0; dt < HD / 32; ++dt) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-            const int d = dt * 32 + col;
+            const int c0 = 4 * dt + 2 * tr_db + (tr_q >> 1);
+            const int byte = (tr_q & 1) * 8;
 #pragma unroll
             for (int gg = 0; gg < 2; ++gg) {
-                const f16x8 va = lds_ld16(vs, tr_off<kTile>(d, 2 * gg + hh));
+                const int r0 = 16 * gg + tr_row, r1 = r0 + 4;
+                const f16x4 lo = lds_tr4(vs, r0 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r0)) << 4) + byte);
+                const f16x4 hi = lds_tr4(vs, r1 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r1)) << 4) + byte);
+                const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 o[dt] = mfma32(va, ph[gg], o[dt]);
                 o[dt] = mfma32(va, pl[gg], o[dt]);
             }
         }
+        // Stage st is free again (every read above has been consumed): refill it.
         __builtin_amdgcn_wave_barrier();
+        if (k + 2 < n_my) issue(my_first + (k + 2) * kKvWaves, st);
     }
+    };
+    if (pages_in_lds)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 
     // Merge the four waves: each publishes (m, l) per row and its O^T tile.
     const float l_w = l_p + __shfl_xor(l_p, 32);
     float *mrow = reinterpret_cast<float *>(smem + kKvWaves * C::WAVE_LDS);
     float *lrow = mrow + kKvWaves * 32;
-    __syncthreads();  // every wave is done with its tile region
+    __syncthreads();  // every wave is done with its ring
     float *ow = reinterpret_cast<float *>(smem + wave * C::WAVE_LDS);  // [HD][32] fp32
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt)
