@@ -7,8 +7,8 @@ inputs already resident in HBM:
 
 * headline (BASELINE config c2): causal MHA forward + backward, batch 4,
   seqlen 4096, 16 heads, head_dim 128, fp16, seed 1.  One step launches the
-  four kernels of the path through the C ABI (fa_fwd, fa_bwd_preprocess,
-  fa_bwd_dq, fa_bwd_dkdv) into preallocated outputs.  ``value`` is the
+  three kernels of the path through the C ABI (fa_fwd; fa_bwd_dq, which also
+  computes the dO.O row sums; fa_bwd_dkdv) into preallocated outputs.  ``value`` is the
   algorithmic TFLOPS of the step: (4 + 10) * b * h * d * pairs / step time.
 * extra, reported in the same line: the same step at seqlen 8192 (seed 5, the
   point the 50 % / 35 % MFMA targets are quoted on) and the paged split-KV
@@ -111,9 +111,9 @@ def train_step_setup(batch, seqlen, heads, hd, seed, device):
     scale = hd ** -0.5
     fa = fa_capi.fwd_args(q, k, v, o, lse, scale, True)
     ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, True)
+    # fa_bwd_dq also computes D = rowsum(dO * O) (the preprocess) for fa_bwd_dkdv.
     launches = [
         ("fwd", lambda: fa_capi.call("fa_fwd", fa)),
-        ("bwd_preprocess", lambda: fa_capi.call("fa_bwd_preprocess", ba)),
         ("bwd_dq", lambda: fa_capi.call("fa_bwd_dq", ba)),
         ("bwd_dkdv", lambda: fa_capi.call("fa_bwd_dkdv", ba)),
     ]
@@ -135,7 +135,7 @@ def train_report(batch, seqlen, heads, hd, ms_step, per):
             byts = 2 * batch * seqlen * heads * hd * 2 + batch * heads * seqlen * 4
             entry["gbs"] = round(byts / (ms * 1e-3) / 1e9, 1)
         kern[name] = entry
-    bwd_ms = per["bwd_preprocess"] + per["bwd_dq"] + per["bwd_dkdv"]
+    bwd_ms = sum(ms for name, ms in per.items() if name.startswith("bwd"))
     return {
         "pairs": pairs,
         "fwd_tflops": round(4 * unit / (per["fwd"] * 1e-3) / 1e12, 1),
@@ -347,7 +347,7 @@ def main():
         "dtype": "fp16",
         "data": "synthetic",
         "config": {"workload": "c2: causal MHA fwd+bwd, batch 4, seqlen 4096, 16 heads, head_dim 128, fp16 "
-                               "N(0,1) seed 1; one step = fa_fwd + fa_bwd_preprocess + fa_bwd_dq + fa_bwd_dkdv",
+                               "N(0,1) seed 1; one step = fa_fwd + fa_bwd_dq (incl. the dO.O row sums) + fa_bwd_dkdv",
                    "batch": b, "seqlen": s, "heads": h, "head_dim": d, "causal": True},
     }
     if args.only == "decode":

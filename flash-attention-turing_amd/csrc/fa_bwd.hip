@@ -26,16 +26,18 @@ constexpr int kBwdThreads = 256;
 
 // ---------------------------------------------------------------------------
 // Preprocess: dsum[b][h][i] = sum_d fp32(O) * fp32(dO); padding rows get 0.
+// One group of KCH threads per row; consecutive groups take consecutive rows of
+// one head so the row sums are written contiguously.  fa_bwd computes the same
+// sums inside the dQ kernel; this standalone kernel serves fa_bwd_preprocess.
 template <int HD>
 __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a) {
     constexpr int KCH = HD / 8;
-    constexpr int ROWS = kBwdThreads / KCH;  // (row, head) pairs per workgroup
-    const int b = blockIdx.y;
+    constexpr int ROWS = kBwdThreads / KCH;  // rows per workgroup
+    const int b = blockIdx.z, h = blockIdx.y;
     const bool packed = a.cu_seqlens_q != nullptr;
     const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
-    const int t = blockIdx.x * ROWS + threadIdx.x / KCH;  // t = i * nheads + h
+    const int i = blockIdx.x * ROWS + threadIdx.x / KCH;
     const int c = threadIdx.x % KCH;
-    const int i = t / a.nheads, h = t - i * a.nheads;
     if (i >= a.lse_seqlen) return;
     float acc = 0.f;
     if (i < si.sq) {
@@ -52,22 +54,22 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a
 }
 
 // ---------------------------------------------------------------------------
-// dQ kernel.
+// dQ kernel: 4 waves x 32 queries of one (batch, head); 64-key blocks of K and
+// V copied HBM -> LDS (two stages, global_load_lds); S^T = K Q^T and
+// dP^T = V dO^T read K, V as natural A operands, dQ^T += K^T dS^T reads K
+// transposed (ds_read_b64_tr_b16).  The prologue computes D = rowsum(dO * O)
+// for the workgroup's rows and stores it for the dK/dV kernel.
 template <int HD>
 struct DqCfg {
-    static constexpr int BM = 128, BN = 64, NT = kBwdThreads, KCH = HD / 8;
-    static constexpr int KN = BN * HD * 2;  // K natural
-    static constexpr int KT = HD * BN * 2;  // K transposed
-    static constexpr int VN = BN * HD * 2;  // V natural
-    static constexpr int STAGE = KN + KT + VN;
-    static constexpr int UNITS = (BN / 4) * KCH;
-    static constexpr int V_LD = BN * KCH / NT;
+    static constexpr int BM = 128, BN = 64, NT = kBwdThreads;
+    static constexpr int TILE = BN * HD * 2;  // K or V tile, natural layout
+    static constexpr int STAGE = 2 * TILE;
 };
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks) {
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks) {
     using C = DqCfg<HD>;
-    constexpr int BM = C::BM, BN = C::BN, NT = C::NT, KCH = C::KCH;
+    constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -86,6 +88,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const fa_bwd_args a, const 
 
     const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, h);
     const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, h);
+    const f16 *opp = (const f16 *)a.o.ptr + base_off(a.o, packed_q, b, si.q_start, h);
     const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, b, si.k_start, hk);
     const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, b, si.k_start, hk);
     f16 *dqp = (f16 *)a.dq.ptr + base_off(a.dq, packed_q, b, si.q_start, h);
@@ -97,66 +100,42 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const fa_bwd_args a, const 
     const int n_blocks = (n_end + BN - 1) / BN;
     const float cs = a.softmax_scale * kLog2e;
 
+    // Q^T, dO^T as B operands (lane: query col, d = 16g + 8hh + 0..7) and this
+    // lane's half of D = sum_d O * dO.
     const int qi = m0 + wave * 32 + col;
     const bool qv = qi < sq;
     f16x8 qB[HD / 16], doB[HD / 16];
+    float dpart = 0.f;
 #pragma unroll
     for (int g = 0; g < HD / 16; ++g) {
         qB[g] = as_h8(qv ? ldg16(qp + int64_t(qi) * a.q.row_stride + 16 * g + 8 * hh) : zero_u4());
         doB[g] = as_h8(qv ? ldg16(dop + int64_t(qi) * a.dout.row_stride + 16 * g + 8 * hh) : zero_u4());
+        const f16x8 ov = as_h8(qv ? ldg16(opp + int64_t(qi) * a.o.row_stride + 16 * g + 8 * hh) : zero_u4());
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dpart += float(ov[t]) * float(doB[g][t]);
     }
+    const float dsum = dpart + __shfl_xor(dpart, 32);
+    if (qv && hh == 0) a.dsum[lrow + qi] = dsum;
     const float lse2 = qv ? a.lse[lrow + qi] * kLog2e : 0.f;
-    const float dsum = qv ? a.dsum[lrow + qi] : 0.f;
+    wait_vmem();  // nothing but the tile copies may be in flight in the loop
 
     f32x16 dq[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) dq[i] = zero16();
 
-    u32x4 kreg[4], vreg[C::V_LD];
-    const bool k_thread = tid < C::UNITS;
-    const int um = tid % (BN / 4), uc = tid / (BN / 4);
-    auto load = [&](int nb) {
-        const int n0 = nb * BN;
-        if (k_thread) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = n0 + 4 * um + r;
-                kreg[r] = key < sk ? ldg16(kp + int64_t(key) * a.k.row_stride + 8 * uc) : zero_u4();
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < C::V_LD; ++i) {
-            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
-            const int key = n0 + row;
-            vreg[i] = key < sk ? ldg16(vp + int64_t(key) * a.v.row_stride + 8 * c) : zero_u4();
-        }
+    auto issue = [&](int nb, int st) {
+        char *ks = smem + st * C::STAGE;
+        dma_tile<HD, BN, NT>(ks, kp, a.k.row_stride, nb * BN, sk - 1, wave, lane);
+        dma_tile<HD, BN, NT>(ks + C::TILE, vp, a.v.row_stride, nb * BN, sk - 1, wave, lane);
     };
-    auto store = [&](int buf) {
-        char *kn = smem + buf * C::STAGE;
-        char *kt = kn + C::KN;
-        char *vn = kt + C::KT;
-        if (k_thread) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) lds_st16(kn, nat_off<HD>(4 * um + r, uc), kreg[r]);
-            tr_store4<BN>(kt, 4 * um, 8 * uc, kreg[0], kreg[1], kreg[2], kreg[3]);
-        }
-#pragma unroll
-        for (int i = 0; i < C::V_LD; ++i) {
-            const int idx = tid + i * NT, row = idx / KCH, c = idx % KCH;
-            lds_st16(vn, nat_off<HD>(row, c), vreg[i]);
-        }
-    };
-
-    if (n_blocks > 0) {
-        load(0);
-        store(0);
-    }
-    __syncthreads();
+    if (n_blocks > 0) issue(0, 0);
 
     const int q_lo = m0 + wave * 32;
     for (int nb = 0; nb < n_blocks; ++nb) {
         const int buf = nb & 1;
-        if (nb + 1 < n_blocks) load(nb + 1);
+        wait_vmem();
+        __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
+        if (nb + 1 < n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
         bool active = true;
         bool need_mask = n0 + BN > sk;
@@ -164,44 +143,38 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const fa_bwd_args a, const 
             if (n0 > q_lo + 31 + causal_off) active = false;
             if (n0 + BN - 1 > q_lo + causal_off) need_mask = true;
         }
-        if (active) {
-            const char *kn = smem + buf * C::STAGE;
-            const char *kt = kn + C::KN;
-            const char *vn = kt + C::KT;
-            f32x16 s[2], dp[2];
+        if (!active) continue;
+        const char *ks = smem + buf * C::STAGE;
+        const char *vs = ks + C::TILE;
+        f32x16 s[2], dp[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                s[t] = zero16();
-                dp[t] = zero16();
-                const int row = t * 32 + sigma(col);
+        for (int t = 0; t < 2; ++t) {
+            s[t] = zero16();
+            dp[t] = zero16();
+            const int row = t * 32 + sigma(col);
 #pragma unroll
-                for (int g = 0; g < HD / 16; ++g) {
-                    s[t] = mfma32(lds_ld16(kn, nat_off<HD>(row, 2 * g + hh)), qB[g], s[t]);
-                    dp[t] = mfma32(lds_ld16(vn, nat_off<HD>(row, 2 * g + hh)), doB[g], dp[t]);
-                }
-            }
-            const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float p = exp2_fast(fmaf(s[t][r], cs, -lse2));
-                    if (need_mask && n0 + t * 32 + acc_lrow(r, hh) > lim) p = 0.f;
-                    s[t][r] = p * (dp[t][r] - dsum);
-                }
-            f16x8 dsB[4];
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) dsB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
-#pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt) {
-                const int d = dt * 32 + col;
-#pragma unroll
-                for (int gg = 0; gg < 4; ++gg)
-                    dq[dt] = mfma32(lds_ld16(kt, tr_off<BN>(d, 2 * gg + hh)), dsB[gg], dq[dt]);
+            for (int g = 0; g < HD / 16; ++g) {
+                const int off = tile_off<HD>(row, 2 * g + hh);
+                s[t] = mfma32(lds_ld16(ks, off), qB[g], s[t]);
+                dp[t] = mfma32(lds_ld16(vs, off), doB[g], dp[t]);
             }
         }
-        if (nb + 1 < n_blocks) store(buf ^ 1);
-        __syncthreads();
+        const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = exp2_fast(fmaf(s[t][r], cs, -lse2));
+                if (need_mask && n0 + t * 32 + acc_lrow(r, hh) > lim) p = 0.f;
+                s[t][r] = p * (dp[t][r] - dsum);
+            }
+        f16x8 dsB[4];
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) dsB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) dq[dt] = mfma32(lds_tr_operand<HD>(ks, 16 * gg, 32 * dt, lane), dsB[gg], dq[dt]);
     }
 
     if (qv) {
@@ -219,20 +192,24 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const fa_bwd_args a, const 
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV kernel.
+// dK/dV kernel: 4 waves x 32 keys of one (batch, KV head); K, V stay in
+// registers as B operands.  For every q-head of the GQA group and every
+// 64-query block that sees these keys, Q, dO, LSE and D are copied HBM -> LDS
+// (two stages); S = Q K^T and dP = dO V^T read Q, dO as natural A operands,
+// dV^T += dO^T P and dK^T += Q^T dS read them transposed.  The group's
+// contributions accumulate in fp32 registers (no per-q-head dK/dV buffers).
+// Needs D (dsum) from the dQ kernel or the preprocess kernel.
 template <int HD>
 struct DkvCfg {
-    static constexpr int BN = 128, BM = 64, NT = kBwdThreads, KCH = HD / 8;
-    static constexpr int QN = BM * HD * 2;  // natural [64][HD]
-    static constexpr int QT = HD * BM * 2;  // transposed [HD][64]
-    static constexpr int STAGE = 2 * QN + 2 * QT + 2 * BM * 4;  // Qn Qt dOn dOt lse2 D
-    static constexpr int UNITS = (BM / 4) * KCH;
+    static constexpr int BN = 128, BM = 64, NT = kBwdThreads;
+    static constexpr int QTILE = BM * HD * 2;             // Q or dO tile, natural layout
+    static constexpr int STAGE = 2 * QTILE + 2 * BM * 4;  // Q, dO, LSE, D
 };
 
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     using C = DkvCfg<HD>;
-    constexpr int BN = C::BN, BM = C::BM;
+    constexpr int BN = C::BN, BM = C::BM, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -264,6 +241,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
         kB[g] = as_h8(kv_ok ? ldg16(kp + int64_t(key) * a.k.row_stride + 16 * g + 8 * hh) : zero_u4());
         vB[g] = as_h8(kv_ok ? ldg16(vp + int64_t(key) * a.v.row_stride + 16 * g + 8 * hh) : zero_u4());
     }
+    wait_vmem();  // nothing but the tile copies may be in flight in the loop
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) {
@@ -276,59 +254,29 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     const int n_qb = max(0, (sq + BM - 1) / BM - m_first);
     const int total = G * n_qb;
 
-    u32x4 qreg[4], doreg[4];
-    float lreg = 0.f;
-    const bool u_thread = tid < C::UNITS;
-    const int um = tid % (BM / 4), uc = tid / (BM / 4);
-    auto load = [&](int j) {
+    // Copy (q-head, query block) j into stage st.  Rows past the sequence
+    // re-read its last row (finite values; their P and dS are zeroed below).
+    auto issue = [&](int j, int st) {
         const int hq = hk * G + j / n_qb;
         const int q0 = (m_first + j % n_qb) * BM;
-        if (u_thread) {
-            const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hq);
-            const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hq);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int q = q0 + 4 * um + r;
-                qreg[r] = q < sq ? ldg16(qp + int64_t(q) * a.q.row_stride + 8 * uc) : zero_u4();
-                doreg[r] = q < sq ? ldg16(dop + int64_t(q) * a.dout.row_stride + 8 * uc) : zero_u4();
-            }
-        }
-        if (tid < 2 * BM) {
-            const int q = q0 + (tid & (BM - 1));
-            const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen;
-            if (tid < BM)
-                lreg = q < sq ? a.lse[lrow + q] * kLog2e : 0.f;
-            else
-                lreg = q < sq ? a.dsum[lrow + q] : 0.f;
-        }
-    };
-    auto store = [&](int buf) {
-        char *qn = smem + buf * C::STAGE;
-        char *qt = qn + C::QN;
-        char *on = qt + C::QT;
-        char *ot = on + C::QN;
-        float *lf = reinterpret_cast<float *>(ot + C::QT);
-        if (u_thread) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                lds_st16(qn, nat_off<HD>(4 * um + r, uc), qreg[r]);
-                lds_st16(on, nat_off<HD>(4 * um + r, uc), doreg[r]);
-            }
-            tr_store4<BM>(qt, 4 * um, 8 * uc, qreg[0], qreg[1], qreg[2], qreg[3]);
-            tr_store4<BM>(ot, 4 * um, 8 * uc, doreg[0], doreg[1], doreg[2], doreg[3]);
-        }
-        if (tid < 2 * BM) lf[tid] = lreg;
+        char *qt = smem + st * C::STAGE;
+        char *ot = qt + C::QTILE;
+        char *lf = ot + C::QTILE;
+        const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hq);
+        const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hq);
+        dma_tile<HD, BM, NT>(qt, qp, a.q.row_stride, q0, sq - 1, wave, lane);
+        dma_tile<HD, BM, NT>(ot, dop, a.dout.row_stride, q0, sq - 1, wave, lane);
+        const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
+        if (wave == 0) g2l4(a.lse + lrow, lf);
+        if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
     };
 
-    if (total > 0) {
-        load(0);
-        store(0);
-    }
-    __syncthreads();
-
+    if (total > 0) issue(0, 0);
     for (int j = 0; j < total; ++j) {
         const int buf = j & 1;
-        if (j + 1 < total) load(j + 1);
+        wait_vmem();
+        __syncthreads();  // block j is in LDS; every wave is done with stage buf ^ 1
+        if (j + 1 < total) issue(j + 1, buf ^ 1);
         const int q0 = (m_first + j % n_qb) * BM;
         bool active = true;
         bool need_mask = q0 + BM > sq || kw0 + 32 > sk;
@@ -336,56 +284,55 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
             if (q0 + BM - 1 + causal_off < kw0) active = false;
             if (kw0 + 31 > q0 + causal_off) need_mask = true;
         }
-        if (active) {
-            const char *qn = smem + buf * C::STAGE;
-            const char *qt = qn + C::QN;
-            const char *on = qt + C::QT;
-            const char *ot = on + C::QN;
-            const float *lf = reinterpret_cast<const float *>(ot + C::QT);
-            f32x16 s[2], dp[2];
+        if (!active) continue;
+        const char *qt = smem + buf * C::STAGE;
+        const char *ot = qt + C::QTILE;
+        const float *lf = reinterpret_cast<const float *>(ot + C::QTILE);
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                s[t] = zero16();
-                dp[t] = zero16();
-                const int row = t * 32 + sigma(col);
+        for (int sub = 0; sub < 2; ++sub) {  // 32-query halves of the block
+            f32x16 s = zero16(), dp = zero16();
+            const int row = sub * 32 + sigma(col);
 #pragma unroll
-                for (int g = 0; g < HD / 16; ++g) {
-                    s[t] = mfma32(lds_ld16(qn, nat_off<HD>(row, 2 * g + hh)), kB[g], s[t]);
-                    dp[t] = mfma32(lds_ld16(on, nat_off<HD>(row, 2 * g + hh)), vB[g], dp[t]);
-                }
+            for (int g = 0; g < HD / 16; ++g) {
+                const int off = tile_off<HD>(row, 2 * g + hh);
+                s = mfma32(lds_ld16(qt, off), kB[g], s);
+                dp = mfma32(lds_ld16(ot, off), vB[g], dp);
             }
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int r8 = 0; r8 < 2; ++r8) {
+                const int ql0 = sub * 32 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
+                const f32x4 l_a = *reinterpret_cast<const f32x4 *>(lf + ql0);
+                const f32x4 l_b = *reinterpret_cast<const f32x4 *>(lf + ql0 + 4);
+                const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + BM + ql0);
+                const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + BM + ql0 + 4);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int ql = t * 32 + acc_lrow(r, hh);
-                    const float l2 = lf[ql], dsum = lf[BM + ql];
-                    float p = exp2_fast(fmaf(s[t][r], cs, -l2));
+                for (int u = 0; u < 8; ++u) {
+                    const int r = 8 * r8 + u;
+                    const float l2 = (u < 4 ? l_a[u] : l_b[u - 4]) * kLog2e;
+                    const float dsum = u < 4 ? d_a[u] : d_b[u - 4];
+                    float p = exp2_fast(fmaf(s[r], cs, -l2));
                     if (need_mask) {
-                        const int q = q0 + ql;
+                        const int q = q0 + ql0 + u;
                         if (q >= sq || !kv_ok || (CAUSAL && key > q + causal_off)) p = 0.f;
                     }
-                    s[t][r] = p;
-                    dp[t][r] = p * (dp[t][r] - dsum);
-                }
-            f16x8 pB[4], dsB[4];
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) {
-                pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
-                dsB[gg] = pack8(dp[gg >> 1], 8 * (gg & 1));
-            }
-#pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt) {
-                const int d = dt * 32 + col;
-#pragma unroll
-                for (int gg = 0; gg < 4; ++gg) {
-                    dv[dt] = mfma32(lds_ld16(ot, tr_off<BM>(d, 2 * gg + hh)), pB[gg], dv[dt]);
-                    dk[dt] = mfma32(lds_ld16(qt, tr_off<BM>(d, 2 * gg + hh)), dsB[gg], dk[dt]);
+                    s[r] = p;
+                    dp[r] = p * (dp[r] - dsum);
                 }
             }
+            f16x8 pB[2], dsB[2];
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) {
+                pB[gg] = pack8(s, 8 * gg);
+                dsB[gg] = pack8(dp, 8 * gg);
+            }
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+                for (int gg = 0; gg < 2; ++gg) {
+                    dv[dt] = mfma32(lds_tr_operand<HD>(ot, sub * 32 + 16 * gg, 32 * dt, lane), pB[gg], dv[dt]);
+                    dk[dt] = mfma32(lds_tr_operand<HD>(qt, sub * 32 + 16 * gg, 32 * dt, lane), dsB[gg], dk[dt]);
+                }
         }
-        if (j + 1 < total) store(buf ^ 1);
-        __syncthreads();
     }
 
     if (kv_ok) {
@@ -424,10 +371,11 @@ static int check_bwd(const fa_bwd_args *p) {
 template <int HD>
 static int launch_preprocess(const fa_bwd_args &a, hipStream_t s) {
     constexpr int ROWS = kBwdThreads / (HD / 8);
-    const int64_t gx = (int64_t(a.lse_seqlen) * a.nheads + ROWS - 1) / ROWS;
+    const int64_t gx = (int64_t(a.lse_seqlen) + ROWS - 1) / ROWS;
     if (gx == 0 || a.batch == 0) return FA_OK;
-    hipLaunchKernelGGL(bwd_preprocess_kernel<HD>, dim3(unsigned(gx), unsigned(a.batch)), dim3(kBwdThreads), 0, s,
-                       a);
+    if (a.nheads > 65535 || a.batch > 65535) return FA_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(bwd_preprocess_kernel<HD>, dim3(unsigned(gx), unsigned(a.nheads), unsigned(a.batch)),
+                       dim3(kBwdThreads), 0, s, a);
     return int(hipGetLastError());
 }
 
@@ -490,9 +438,8 @@ extern "C" int fa_bwd_dkdv(const fa_bwd_args *args, void *stream) {
 }
 
 extern "C" int fa_bwd(const fa_bwd_args *args, void *stream) {
-    int rc = fa_bwd_preprocess(args, stream);
-    if (rc) return rc;
-    rc = fa_bwd_dq(args, stream);
+    // The dQ kernel also writes D = rowsum(dO * O) for the dK/dV kernel.
+    int rc = fa_bwd_dq(args, stream);
     if (rc) return rc;
     return fa_bwd_dkdv(args, stream);
 }

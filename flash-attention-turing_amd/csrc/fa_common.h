@@ -135,6 +135,21 @@ __device__ __forceinline__ void g2l16(const void *g, char *lds_base) {
         : "v"(g), "s"(l)
         : "memory");
 }
+// global_load_lds_dword: lane l's 4 bytes at `g` land at lds_base + 4*l.
+__device__ __forceinline__ void g2l4(const void *g, char *lds_base) {
+    const uint32_t l =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds_base);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(l)
+        : "memory");
+}
+
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // s_waitcnt vmcnt(N), N < 64.
@@ -153,17 +168,55 @@ __device__ __forceinline__ f16x4 lds_tr4(const char *base, int off) {
     return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + off)));
 }
 
-// Natural [rows][KCH chunks] tiles read as MFMA A operands (rows sigma(0..31)
-// at one chunk): chunk c of row r sits at chunk c ^ swz_rows(r).
+// Placement of a natural [rows][KCH 16-byte chunks] fp16 tile in LDS: chunk c
+// of row r sits at chunk c ^ swz(r).  The XOR masks are chosen so that both
+// read patterns the kernels use are bank-conflict free (checked for 32 and
+// 64 four-byte banks, i.e. 8 or 16 lanes per ds_read_b128 phase and 16 or 32
+// lanes per ds_read_b64 phase):
+//   * MFMA A-operand rows: lanes read rows sigma(0..31) at one chunk pair;
+//   * lds_tr4 transposed reads: 8 rows x 64 bytes per instruction.
+// At head_dim 64 (8 chunks per row) a 16-lane b128 phase cannot be conflict
+// free; the 8-lane phases are.
 template <int KCH>
-__device__ __forceinline__ int swz_rows(int row) {
-    return sigma(row) & (KCH - 1);
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (KCH == 16)
+        return ((row & 1) ? 4 : 0) ^ ((row & 2) ? 10 : 0) ^ ((row & 4) ? 2 : 0) ^ ((row & 8) ? 1 : 0);
+    else
+        return ((row & 1) ? 2 : 0) ^ ((row & 2) ? 4 : 0) ^ ((row & 8) ? 1 : 0);
 }
-// Natural tiles read with lds_tr4 (per instruction 8 rows x 64 bytes, 4 rows x
-// 32 bytes per 16 lanes): conflict-free placement for 16- and 32-lane phases.
-template <int KCH>
-__device__ __forceinline__ int swz_tr(int row) {
-    return KCH == 16 ? (((row & 1) ? 4 : 0) ^ ((row & 2) ? 10 : 0)) : (((row & 1) ? 2 : 0) ^ ((row & 2) ? 4 : 0));
+// Byte offset of (row, chunk) in such a tile.
+template <int HD>
+__device__ __forceinline__ int tile_off(int row, int chunk) {
+    return row * (HD * 2) + ((chunk ^ swz<HD / 8>(row)) << 4);
+}
+
+// MFMA A operand (32 x 16 fp16) of the transposed tile: lane (m, h) gets
+// column d0 + m of rows r0 + 8h + 0..7 (the key / query order a chained
+// accumulator supplies, see the header comment).
+template <int HD>
+__device__ __forceinline__ f16x8 lds_tr_operand(const char *tile, int r0, int d0, int lane) {
+    const int j = (lane & 15) >> 2, q = lane & 3, db = (lane >> 4) & 1, h = lane >> 5;
+    const int row = r0 + 8 * h + j, col = d0 + 16 * db + 4 * q;
+    const int byte = (col & 7) * 2;
+    const f16x4 lo = lds_tr4(tile, tile_off<HD>(row, col >> 3) + byte);
+    const f16x4 hi = lds_tr4(tile, tile_off<HD>(row + 4, col >> 3) + byte);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Copy rows [row0, row0 + ROWS) of a [rows][HD] fp16 source (row stride rs,
+// rows clamped to <= last_row) into a swizzled natural tile with DMA: the NT
+// threads of the workgroup each move ROWS*HD/8/NT chunks.
+template <int HD, int ROWS, int NT>
+__device__ __forceinline__ void dma_tile(char *tile, const f16 *src, int64_t rs, int row0, int last_row, int wave,
+                                         int lane) {
+    constexpr int KCH = HD / 8, CPT = ROWS * KCH / NT, WAVES = NT / 64;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int base = (i * WAVES + wave) * 64;
+        const int p = base + lane, row = p / KCH, cs = p % KCH;
+        const int64_t r = min(row0 + row, last_row);
+        g2l16(src + r * rs + 8 * (cs ^ swz<KCH>(row)), tile + base * 16);
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -31,13 +31,12 @@ struct FwdCfg {
     static constexpr int KCH = HD / 8;            // 16-byte chunks per row
     static constexpr int TILE = BN * HD * 2;      // one K or V tile
     static constexpr int STAGE = 2 * TILE;        // K tile, then V tile
-    static constexpr int CPT = BN * KCH / NT;     // chunks per thread per tile
 };
 
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
     using C = FwdCfg<HD>;
-    constexpr int BM = C::BM, BN = C::BN, NT = C::NT, KCH = C::KCH;
+    constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -95,27 +94,13 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
     float m_t = -INFINITY;  // running max of scale*log2(e)*S for this lane's query
     float l_p = 0.f;        // partial row sum over this lane half's keys
 
-    // Copy of key block nb into stage st: chunk p = (i*4 + wave)*64 + lane of
-    // each tile holds chunk (p % KCH) ^ swz of row p / KCH.  Rows past the
-    // sequence re-read its last key (finite values; masked below).
+    // Copy of key block nb into stage st.  Rows past the sequence re-read its
+    // last key (finite values; masked below).
     auto issue = [&](int nb, int st) {
         char *ks = smem + st * C::STAGE;
-        char *vs = ks + C::TILE;
-        const int n0 = nb * BN;
-#pragma unroll
-        for (int i = 0; i < C::CPT; ++i) {
-            const int base = (i * 4 + wave) * 64;
-            const int p = base + lane, row = p / KCH, cs = p % KCH;
-            const int64_t key = min(n0 + row, sk - 1);
-            g2l16(kp + key * krs + 8 * (cs ^ swz_rows<KCH>(row)), ks + base * 16);
-            g2l16(vp + key * vrs + 8 * (cs ^ swz_tr<KCH>(row)), vs + base * 16);
-        }
+        dma_tile<HD, BN, NT>(ks, kp, krs, nb * BN, sk - 1, wave, lane);
+        dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, nb * BN, sk - 1, wave, lane);
     };
-
-    // Per-lane parts of the transposed V reads (see lds_tr4): group lane
-    // s = 4*j + q points at row 8*hh + j, columns 16*db + 4*q of a 32-column slab.
-    const int tr_j = (lane & 15) >> 2, tr_q = lane & 3, tr_db = (lane >> 4) & 1;
-    const int tr_row = 8 * hh + tr_j;
 
     if (n_blocks > 0) issue(0, 0);
 
@@ -141,10 +126,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
         for (int kt = 0; kt < 2; ++kt) {
             s[kt] = zero16();
             const int row = kt * 32 + sigma(col);
-            const int rbase = row * (HD * 2), sw = swz_rows<KCH>(row);
 #pragma unroll
-            for (int g = 0; g < HD / 16; ++g)
-                s[kt] = mfma32(lds_ld16(ks, rbase + (((2 * g + hh) ^ sw) << 4)), qB[g], s[kt]);
+            for (int g = 0; g < HD / 16; ++g) s[kt] = mfma32(lds_ld16(ks, tile_off<HD>(row, 2 * g + hh)), qB[g], s[kt]);
         }
 
         float mx = -INFINITY;
@@ -197,18 +180,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
 #pragma unroll
         for (int gg = 0; gg < 4; ++gg) pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
 #pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt) {
-            const int c0 = 4 * dt + 2 * tr_db + (tr_q >> 1);
-            const int byte = (tr_q & 1) * 8;
+        for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg) {
-                const int r0 = 16 * gg + tr_row, r1 = r0 + 4;
-                const f16x4 lo = lds_tr4(vs, r0 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r0)) << 4) + byte);
-                const f16x4 hi = lds_tr4(vs, r1 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r1)) << 4) + byte);
-                const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[dt] = mfma32(va, pB[gg], o[dt]);
-            }
-        }
+            for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(lds_tr_operand<HD>(vs, 16 * gg, 32 * dt, lane), pB[gg], o[dt]);
     }
 
     // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.

@@ -84,14 +84,13 @@ struct KvCfg {
     static constexpr int STAGE = 2 * TILE;              // K tile, then V tile
     static constexpr int NST = 2;                       // ring stages per wave
     static constexpr int WAVE_LDS = NST * STAGE;        // also holds HD x 32 fp32 at the merge
-    static constexpr int CPW = kTile * KCH / 64;        // DMA instructions per lane per tile (K or V)
+    static constexpr int CPW = kTile * KCH / 64;        // copies per lane per tile (K or V)
     static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
 };
 
 template <int HD>
 __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a, const int row_tiles) {
     using C = KvCfg<HD>;
-    constexpr int KCH = C::KCH;
     __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
     __shared__ int pages[C::MAX_PAGES];
 
@@ -155,8 +154,6 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
     __syncthreads();
 
     const int64_t krs = a.k_cache.row_stride, vrs = a.v_cache.row_stride;
-    const int tr_j = (lane & 15) >> 2, tr_q = lane & 3, tr_db = (lane >> 4) & 1;
-    const int tr_row = 8 * hh + tr_j;
 
     // The tile loop, instantiated twice: with the split's page ids in LDS (and
     // no other vector-memory load while copies are in flight), and a fallback
@@ -186,14 +183,8 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
         const f16 *vb = (const f16 *)a.v_cache.ptr + voff + int64_t(hk) * a.v_cache.head_stride;
         char *ks = smem + (wave * C::NST + st) * C::STAGE;
         char *vs = ks + C::TILE;
-        const int rmax = L - 1 - p0;
-#pragma unroll
-        for (int i = 0; i < C::CPW; ++i) {
-            const int p = i * 64 + lane, r = p / KCH, cs = p % KCH;
-            const int rr = min(r, rmax);
-            g2l16(kb + int64_t(rr) * krs + 8 * (cs ^ swz_rows<KCH>(r)), ks + i * 1024);
-            g2l16(vb + int64_t(rr) * vrs + 8 * (cs ^ swz_tr<KCH>(r)), vs + i * 1024);
-        }
+        dma_tile<HD, kTile, 64>(ks, kb, krs, 0, L - 1 - p0, 0, lane);
+        dma_tile<HD, kTile, 64>(vs, vb, vrs, 0, L - 1 - p0, 0, lane);
     };
 
     if (n_my > 0) issue(my_first, 0);
@@ -208,12 +199,8 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
         const char *vs = ks + C::TILE;
         const int p0 = (my_first + k * kKvWaves) * kTile;
         f32x16 s = zero16();
-        {
-            const int r = sigma(col);
-            const int rbase = r * (HD * 2), sw = swz_rows<KCH>(r);
 #pragma unroll
-            for (int g = 0; g < HD / 16; ++g) s = mfma32(lds_ld16(ks, rbase + (((2 * g + hh) ^ sw) << 4)), qB[g], s);
-        }
+        for (int g = 0; g < HD / 16; ++g) s = mfma32(lds_ld16(ks, tile_off<HD>(sigma(col), 2 * g + hh)), qB[g], s);
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -250,14 +237,9 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
         for (int dt = 0; dt < HD / 32; ++dt) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-            const int c0 = 4 * dt + 2 * tr_db + (tr_q >> 1);
-            const int byte = (tr_q & 1) * 8;
 #pragma unroll
             for (int gg = 0; gg < 2; ++gg) {
-                const int r0 = 16 * gg + tr_row, r1 = r0 + 4;
-                const f16x4 lo = lds_tr4(vs, r0 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r0)) << 4) + byte);
-                const f16x4 hi = lds_tr4(vs, r1 * (HD * 2) + ((c0 ^ swz_tr<KCH>(r1)) << 4) + byte);
-                const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                const f16x8 va = lds_tr_operand<HD>(vs, 16 * gg, 32 * dt, lane);
                 o[dt] = mfma32(va, ph[gg], o[dt]);
                 o[dt] = mfma32(va, pl[gg], o[dt]);
             }
