@@ -205,7 +205,8 @@ __device__ __forceinline__ f16x8 lds_tr_operand(const char *tile, int r0, int d0
 
 // Copy rows [row0, row0 + ROWS) of a [rows][HD] fp16 source (row stride rs,
 // rows clamped to <= last_row) into a swizzled natural tile with DMA: the NT
-// threads of the workgroup each move ROWS*HD/8/NT chunks.
+// threads of the workgroup each move ROWS*HD/8/NT chunks.  General form (any
+// row0, clamping per row); TileCopier below is the fast path.
 template <int HD, int ROWS, int NT>
 __device__ __forceinline__ void dma_tile(char *tile, const f16 *src, int64_t rs, int row0, int last_row, int wave,
                                          int lane) {
@@ -218,6 +219,61 @@ __device__ __forceinline__ void dma_tile(char *tile, const f16 *src, int64_t rs,
         g2l16(src + r * rs + 8 * (cs ^ swz<KCH>(row)), tile + base * 16);
     }
 }
+
+// Unclamped tile copy with the per-lane source offsets computed once: copy i
+// of a lane moves chunk cs of row row_l + i * (NT / KCH); NT / KCH is a
+// multiple of 16, so the swizzle of every copy equals that of row_l.
+template <int HD, int ROWS, int NT>
+struct TileCopier {
+    static constexpr int KCH = HD / 8, CPT = ROWS * KCH / NT, WAVES = NT / 64, RSTEP = NT / KCH;
+    static_assert(RSTEP % 16 == 0, "row step must keep the swizzle");
+    int64_t goff;  // elements from row 0 of the tile to this lane's chunk of copy 0
+    int lds0;      // byte offset of copy 0's wave chunk block in the tile
+    __device__ __forceinline__ void init(int64_t rs, int wave, int lane) {
+        const int p = wave * 64 + lane, row = p / KCH, cs = p % KCH;
+        goff = int64_t(row) * rs + 8 * (cs ^ swz<KCH>(row));
+        lds0 = wave * 64 * 16;
+    }
+    // src_row0: element pointer of the tile's first row (wave-uniform).
+    __device__ __forceinline__ void copy(char *tile, const f16 *src_row0, int64_t rs) const {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) g2l16(src_row0 + goff + int64_t(i) * RSTEP * rs, tile + lds0 + i * WAVES * 1024);
+    }
+};
+
+// Per-lane LDS byte offsets of the MFMA operand reads from swizzled natural
+// tiles, computed once per kernel.  A chunk index c = 2g + h (or 4dt + x) XOR
+// a per-lane swizzle equals the g = 0 (dt = 0) chunk XOR (g << 1) (dt << 2),
+// so every read is one v_xor plus a ds_read with an immediate row offset.
+template <int HD>
+struct TileReader {
+    int a_base;      // A operand: row sigma(col), chunk hh (g = 0)
+    int tr_base[2];  // transposed operand: rows 8h + j and 8h + j + 4, column block of dt = 0
+    __device__ __forceinline__ void init(int lane) {
+        constexpr int KCH = HD / 8;
+        const int col = lane & 31, h = lane >> 5;
+        const int row = sigma(col);
+        a_base = row * (HD * 2) + (((h ^ swz<KCH>(row)) & (KCH - 1)) << 4);
+        const int j = (lane & 15) >> 2, q = lane & 3, db = (lane >> 4) & 1;
+        const int x = 2 * db + (q >> 1), byte = (q & 1) * 8;
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+            const int r = 8 * h + j + 4 * hs;
+            tr_base[hs] = r * (HD * 2) + (((x ^ swz<KCH>(r)) & (KCH - 1)) << 4) + byte;
+        }
+    }
+    // A operand (32 x 16): lane (m, h) gets chunk 2g + h of row r0 + sigma(m); r0 % 32 == 0.
+    __device__ __forceinline__ f16x8 a_operand(const char *tile, int r0, int g) const {
+        return lds_ld16(tile + r0 * (HD * 2), a_base ^ (g << 5));
+    }
+    // Transposed A operand: lane (m, h) gets column 32*dt + m of rows r0 + 8h + 0..7; r0 % 16 == 0.
+    __device__ __forceinline__ f16x8 tr_operand(const char *tile, int r0, int dt) const {
+        const char *t = tile + r0 * (HD * 2);
+        const f16x4 lo = lds_tr4(t, tr_base[0] ^ (dt << 6));
+        const f16x4 hi = lds_tr4(t, tr_base[1] ^ (dt << 6));
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+};
 
 // ---------------------------------------------------------------------------
 // Global memory.

@@ -19,6 +19,8 @@
 // P^T feeds the O^T += V^T P^T MFMAs directly from the accumulators (see
 // fa_common.h).  Two workgroups share a CU (64 KB LDS each at head_dim 128),
 // so one wave's softmax overlaps the other's MFMAs on each SIMD.
+#include <type_traits>
+
 #include "fa_common.h"
 
 namespace fa {
@@ -33,13 +35,21 @@ struct FwdCfg {
     static constexpr int STAGE = 2 * TILE;        // K tile, then V tile
 };
 
+// Rescale threshold of the online softmax (log2 units): the running maximum
+// a row's probabilities are taken against is only raised when a new score
+// exceeds it by more than this, so P = exp2(S*c - m) <= 2^8 (exact in fp16
+// up to rounding, like any P in [0, 1]) and O, l are rescaled rarely.  The
+// final O / l and LSE = m + log2(l) do not depend on which m was used.
+constexpr float kRescaleLog2 = 8.f;
+
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
     using C = FwdCfg<HD>;
     constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int col = lane & 31, hh = lane >> 5;
 
     // Causal blocks are issued heaviest (largest m block) first.
@@ -87,94 +97,92 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
         if (neg) v = neg_h8(v);
         qB[g] = as_h8(v);
     }
+    wait_vmem();  // only the tile copies are in flight inside the loop
 
     f32x16 o[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
-    float m_t = -INFINITY;  // running max of scale*log2(e)*S for this lane's query
+    float m_t = -INFINITY;  // reference max of scale*log2(e)*S for this lane's query
     float l_p = 0.f;        // partial row sum over this lane half's keys
 
-    // Copy of key block nb into stage st.  Rows past the sequence re-read its
-    // last key (finite values; masked below).
+    TileReader<HD> rd;
+    rd.init(lane);
+    TileCopier<HD, BN, NT> kcp, vcp;
+    kcp.init(krs, wave, lane);
+    vcp.init(vrs, wave, lane);
+    // Copy of key block nb into stage st.  A block that runs past the
+    // sequence re-reads its last key for the missing rows (masked below).
     auto issue = [&](int nb, int st) {
         char *ks = smem + st * C::STAGE;
-        dma_tile<HD, BN, NT>(ks, kp, krs, nb * BN, sk - 1, wave, lane);
-        dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, nb * BN, sk - 1, wave, lane);
+        const int n0 = nb * BN;
+        if (n0 + BN <= sk) {
+            kcp.copy(ks, kp + int64_t(n0) * krs, krs);
+            vcp.copy(ks + C::TILE, vp + int64_t(n0) * vrs, vrs);
+        } else {
+            dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
+            dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
+        }
     };
 
-    if (n_blocks > 0) issue(0, 0);
-
     const int q_lo = m0 + wave * 32;
-    for (int nb = 0; nb < n_blocks; ++nb) {
+    // One key block: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASK is a
+    // compile-time switch so the blocks away from the causal diagonal and
+    // the sequence end carry no masking work at all.
+    auto block = [&](int nb, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = nb & 1;
         wait_vmem();
         __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
         if (nb + 1 < n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
-
-        bool active = true;
-        bool need_mask = n0 + BN > sk;
-        if (CAUSAL) {
-            if (n0 > q_lo + 31 + causal_off) active = false;
-            if (n0 + BN - 1 > q_lo + causal_off) need_mask = true;
-        }
-        if (!active) continue;
+        if (CAUSAL && MASK && n0 > q_lo + 31 + causal_off) return;  // no visible key for this wave
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
         f32x16 s[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            s[kt] = zero16();
-            const int row = kt * 32 + sigma(col);
+            s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
 #pragma unroll
-            for (int g = 0; g < HD / 16; ++g) s[kt] = mfma32(lds_ld16(ks, tile_off<HD>(row, 2 * g + hh)), qB[g], s[kt]);
+            for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
         }
-
-        float mx = -INFINITY;
-        if (need_mask) {
-            const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
+        if constexpr (MASK) {
+            const int lim = (CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1) - n0;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    if (n0 + kt * 32 + acc_lrow(r, hh) > lim) s[kt][r] = -INFINITY;
+                    if (kt * 32 + acc_lrow(r, hh) > lim) s[kt][r] = -INFINITY;
         }
+        float mx = s[0][0];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
-        const float m_new = fmaxf(m_t, mx_t);
-        const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        float rs = 0.f;
-        if (need_mask) {
+        const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
+        if (__builtin_amdgcn_ballot_w64(mx_t > m_t + kRescaleLog2) != 0) {
+            const float m_new = fmaxf(m_t, mx_t);
+            const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
+            l_p *= alpha;
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float x = s[kt][r];
-                    const float p = x == -INFINITY ? 0.f : exp2_fast(fmaf(x, cscale, -m_use));
-                    s[kt][r] = p;
-                    rs += p;
-                }
-        } else {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float p = exp2_fast(fmaf(s[kt][r], cscale, -m_use));
-                    s[kt][r] = p;
-                    rs += p;
-                }
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            m_t = m_new;
         }
-        l_p = l_p * alpha + rs;
-        m_t = m_new;
+        const float m_use = m_t == -INFINITY ? 0.f : m_t;
+        float rs = 0.f;
 #pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            for (int r = 0; r < 16; ++r) {
+                const float x = s[kt][r];
+                float p = exp2_fast(fmaf(x, cscale, -m_use));
+                if constexpr (MASK) p = x == -INFINITY ? 0.f : p;
+                s[kt][r] = p;
+                rs += p;
+            }
+        l_p += rs;
 
         f16x8 pB[4];
 #pragma unroll
@@ -182,8 +190,16 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(lds_tr_operand<HD>(vs, 16 * gg, 32 * dt, lane), pB[gg], o[dt]);
-    }
+            for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(rd.tr_operand(vs, 16 * gg, dt), pB[gg], o[dt]);
+    };
+
+    // Blocks [0, n_full) need no mask for any wave of the workgroup: every key
+    // is below the sequence end and at or below the diagonal of the first query.
+    int n_full = min(n_blocks, sk / BN);
+    if (CAUSAL) n_full = min(n_full, max(0, (m0 + causal_off + 1) / BN));
+    if (n_blocks > 0) issue(0, 0);
+    for (int nb = 0; nb < n_full; ++nb) block(nb, std::false_type{});
+    for (int nb = n_full; nb < n_blocks; ++nb) block(nb, std::true_type{});
 
     // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
     const float l_tot = l_p + __shfl_xor(l_p, 32);
