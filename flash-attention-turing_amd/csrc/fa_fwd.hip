@@ -35,13 +35,12 @@ struct FwdCfg {
     static constexpr int STAGE = 2 * TILE;        // K tile, then V tile
 };
 
-// Rescale threshold of the online softmax (log2 units): the running maximum
-// a row's probabilities are taken against is only raised when a new score
-// exceeds it by more than this, so P = exp2(S*c - m) <= 2^8 (exact in fp16
-// up to rounding, like any P in [0, 1]) and O, l are rescaled rarely.  The
-// final O / l and LSE = m + log2(l) do not depend on which m was used.
-constexpr float kRescaleLog2 = 8.f;
-
+// The running maximum a row's probabilities are taken against is raised (and
+// O, l rescaled) only in the blocks where some row of the wave finds a larger
+// score; the wave skips the rescale otherwise.  The maximum is never left
+// stale: with P = exp2(S*c - m) the row's largest probability is exactly 1,
+// which keeps the fp16 rounding of P (and so O's error) at the reference's
+// level for sharply peaked rows.
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
     using C = FwdCfg<HD>;
@@ -160,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
-        if (__builtin_amdgcn_ballot_w64(mx_t > m_t + kRescaleLog2) != 0) {
+        if (__builtin_amdgcn_ballot_w64(mx_t > m_t) != 0) {
             const float m_new = fmaxf(m_t, mx_t);
             const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
             l_p *= alpha;
