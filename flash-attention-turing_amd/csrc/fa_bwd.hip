@@ -18,6 +18,8 @@
 // feeds dQ^T += K^T dS^T straight from the accumulators.
 // dK/dV kernel: 4 waves x 32 keys; S = Q K^T and dP = dO V^T put queries on
 // M so P and dS feed dV^T += dO^T P and dK^T += Q^T dS.
+#include <type_traits>
+
 #include "fa_common.h"
 
 namespace fa {
@@ -72,7 +74,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int col = lane & 31, hh = lane >> 5;
     const int bh_count = a.batch * a.nheads;
     const int bh = blockIdx.x % bh_count;
@@ -93,6 +96,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, b, si.k_start, hk);
     f16 *dqp = (f16 *)a.dq.ptr + base_off(a.dq, packed_q, b, si.q_start, h);
     const int64_t lrow = (int64_t(b) * a.nheads + h) * a.lse_seqlen;
+    const int64_t krs = a.k.row_stride, vrs = a.v.row_stride;
 
     const int causal_off = sk - sq;
     int n_end = sk;
@@ -117,55 +121,58 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     const float dsum = dpart + __shfl_xor(dpart, 32);
     if (qv && hh == 0) a.dsum[lrow + qi] = dsum;
     const float lse2 = qv ? a.lse[lrow + qi] * kLog2e : 0.f;
-    wait_vmem();  // nothing but the tile copies may be in flight in the loop
+    wait_vmem();  // only the tile copies are in flight inside the loop
 
     f32x16 dq[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) dq[i] = zero16();
 
+    TileReader<HD> rd;
+    rd.init(lane);
+    TileCopier<HD, BN, NT> kcp, vcp;
+    kcp.init(krs, wave, lane);
+    vcp.init(vrs, wave, lane);
     auto issue = [&](int nb, int st) {
         char *ks = smem + st * C::STAGE;
-        dma_tile<HD, BN, NT>(ks, kp, a.k.row_stride, nb * BN, sk - 1, wave, lane);
-        dma_tile<HD, BN, NT>(ks + C::TILE, vp, a.v.row_stride, nb * BN, sk - 1, wave, lane);
+        const int n0 = nb * BN;
+        if (n0 + BN <= sk) {
+            kcp.copy(ks, kp + int64_t(n0) * krs, krs);
+            vcp.copy(ks + C::TILE, vp + int64_t(n0) * vrs, vrs);
+        } else {
+            dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
+            dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
+        }
     };
-    if (n_blocks > 0) issue(0, 0);
 
     const int q_lo = m0 + wave * 32;
-    for (int nb = 0; nb < n_blocks; ++nb) {
+    auto block = [&](int nb, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = nb & 1;
         wait_vmem();
         __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
         if (nb + 1 < n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
-        bool active = true;
-        bool need_mask = n0 + BN > sk;
-        if (CAUSAL) {
-            if (n0 > q_lo + 31 + causal_off) active = false;
-            if (n0 + BN - 1 > q_lo + causal_off) need_mask = true;
-        }
-        if (!active) continue;
+        if (CAUSAL && MASK && n0 > q_lo + 31 + causal_off) return;  // no visible key for this wave
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
         f32x16 s[2], dp[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            s[t] = zero16();
-            dp[t] = zero16();
-            const int row = t * 32 + sigma(col);
+            s[t] = mfma32(rd.a_operand(ks, 32 * t, 0), qB[0], zero16());
+            dp[t] = mfma32(rd.a_operand(vs, 32 * t, 0), doB[0], zero16());
 #pragma unroll
-            for (int g = 0; g < HD / 16; ++g) {
-                const int off = tile_off<HD>(row, 2 * g + hh);
-                s[t] = mfma32(lds_ld16(ks, off), qB[g], s[t]);
-                dp[t] = mfma32(lds_ld16(vs, off), doB[g], dp[t]);
+            for (int g = 1; g < HD / 16; ++g) {
+                s[t] = mfma32(rd.a_operand(ks, 32 * t, g), qB[g], s[t]);
+                dp[t] = mfma32(rd.a_operand(vs, 32 * t, g), doB[g], dp[t]);
             }
         }
-        const int lim = CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1;
+        const int lim = (CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1) - n0;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float p = exp2_fast(fmaf(s[t][r], cs, -lse2));
-                if (need_mask && n0 + t * 32 + acc_lrow(r, hh) > lim) p = 0.f;
+                if constexpr (MASK) p = t * 32 + acc_lrow(r, hh) > lim ? 0.f : p;
                 s[t][r] = p * (dp[t][r] - dsum);
             }
         f16x8 dsB[4];
@@ -174,8 +181,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg) dq[dt] = mfma32(lds_tr_operand<HD>(ks, 16 * gg, 32 * dt, lane), dsB[gg], dq[dt]);
-    }
+            for (int gg = 0; gg < 4; ++gg) dq[dt] = mfma32(rd.tr_operand(ks, 16 * gg, dt), dsB[gg], dq[dt]);
+    };
+
+    // Blocks [0, n_full) are fully visible to every row of the workgroup.
+    int n_full = min(n_blocks, sk / BN);
+    if (CAUSAL) n_full = min(n_full, max(0, (m0 + causal_off + 1) / BN));
+    if (n_blocks > 0) issue(0, 0);
+    for (int nb = 0; nb < n_full; ++nb) block(nb, std::false_type{});
+    for (int nb = n_full; nb < n_blocks; ++nb) block(nb, std::true_type{});
 
     if (qv) {
         f16 *row = dqp + int64_t(qi) * a.dq.row_stride;
@@ -212,7 +226,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     constexpr int BN = C::BN, BM = C::BM, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int col = lane & 31, hh = lane >> 5;
     const int bh_count = a.batch * a.nheads_k;
     const int bhk = blockIdx.x % bh_count;
@@ -231,6 +246,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     f16 *dvp = (f16 *)a.dv.ptr + base_off(a.dv, packed_k, b, si.k_start, hk);
     const int causal_off = sk - sq;
     const float cs = a.softmax_scale * kLog2e;
+    const int64_t qrs = a.q.row_stride, dors = a.dout.row_stride;
 
     const int kw0 = k0 + wave * 32;
     const int key = kw0 + col;
@@ -241,7 +257,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
         kB[g] = as_h8(kv_ok ? ldg16(kp + int64_t(key) * a.k.row_stride + 16 * g + 8 * hh) : zero_u4());
         vB[g] = as_h8(kv_ok ? ldg16(vp + int64_t(key) * a.v.row_stride + 16 * g + 8 * hh) : zero_u4());
     }
-    wait_vmem();  // nothing but the tile copies may be in flight in the loop
+    wait_vmem();  // only the tile copies are in flight inside the loop
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) {
@@ -254,6 +270,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     const int n_qb = max(0, (sq + BM - 1) / BM - m_first);
     const int total = G * n_qb;
 
+    TileReader<HD> rd;
+    rd.init(lane);
+    TileCopier<HD, BM, NT> qcp, ocp;
+    qcp.init(qrs, wave, lane);
+    ocp.init(dors, wave, lane);
     // Copy (q-head, query block) j into stage st.  Rows past the sequence
     // re-read its last row (finite values; their P and dS are zeroed below).
     auto issue = [&](int j, int st) {
@@ -264,39 +285,34 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
         char *lf = ot + C::QTILE;
         const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hq);
         const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hq);
-        dma_tile<HD, BM, NT>(qt, qp, a.q.row_stride, q0, sq - 1, wave, lane);
-        dma_tile<HD, BM, NT>(ot, dop, a.dout.row_stride, q0, sq - 1, wave, lane);
+        if (q0 + BM <= sq) {
+            qcp.copy(qt, qp + int64_t(q0) * qrs, qrs);
+            ocp.copy(ot, dop + int64_t(q0) * dors, dors);
+        } else {
+            dma_tile<HD, BM, NT>(qt, qp, qrs, q0, sq - 1, wave, lane);
+            dma_tile<HD, BM, NT>(ot, dop, dors, q0, sq - 1, wave, lane);
+        }
         const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
         if (wave == 0) g2l4(a.lse + lrow, lf);
         if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
     };
 
-    if (total > 0) issue(0, 0);
-    for (int j = 0; j < total; ++j) {
+    // One (q-head, query block): S = Q K^T and dP = dO V^T per 32-query half,
+    // P, dS, then dV^T += dO^T P and dK^T += Q^T dS.
+    auto block = [&](int j, int q0, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = j & 1;
-        wait_vmem();
-        __syncthreads();  // block j is in LDS; every wave is done with stage buf ^ 1
-        if (j + 1 < total) issue(j + 1, buf ^ 1);
-        const int q0 = (m_first + j % n_qb) * BM;
-        bool active = true;
-        bool need_mask = q0 + BM > sq || kw0 + 32 > sk;
-        if (CAUSAL) {
-            if (q0 + BM - 1 + causal_off < kw0) active = false;
-            if (kw0 + 31 > q0 + causal_off) need_mask = true;
-        }
-        if (!active) continue;
         const char *qt = smem + buf * C::STAGE;
         const char *ot = qt + C::QTILE;
         const float *lf = reinterpret_cast<const float *>(ot + C::QTILE);
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {  // 32-query halves of the block
-            f32x16 s = zero16(), dp = zero16();
-            const int row = sub * 32 + sigma(col);
+            f32x16 s = mfma32(rd.a_operand(qt, 32 * sub, 0), kB[0], zero16());
+            f32x16 dp = mfma32(rd.a_operand(ot, 32 * sub, 0), vB[0], zero16());
 #pragma unroll
-            for (int g = 0; g < HD / 16; ++g) {
-                const int off = tile_off<HD>(row, 2 * g + hh);
-                s = mfma32(lds_ld16(qt, off), kB[g], s);
-                dp = mfma32(lds_ld16(ot, off), vB[g], dp);
+            for (int g = 1; g < HD / 16; ++g) {
+                s = mfma32(rd.a_operand(qt, 32 * sub, g), kB[g], s);
+                dp = mfma32(rd.a_operand(ot, 32 * sub, g), vB[g], dp);
             }
 #pragma unroll
             for (int r8 = 0; r8 < 2; ++r8) {
@@ -311,9 +327,10 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
                     const float l2 = (u < 4 ? l_a[u] : l_b[u - 4]) * kLog2e;
                     const float dsum = u < 4 ? d_a[u] : d_b[u - 4];
                     float p = exp2_fast(fmaf(s[r], cs, -l2));
-                    if (need_mask) {
+                    if constexpr (MASK) {
                         const int q = q0 + ql0 + u;
-                        if (q >= sq || !kv_ok || (CAUSAL && key > q + causal_off)) p = 0.f;
+                        const bool dead = q >= sq || !kv_ok || (CAUSAL && key > q + causal_off);
+                        p = dead ? 0.f : p;
                     }
                     s[r] = p;
                     dp[r] = p * (dp[r] - dsum);
@@ -329,10 +346,24 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
             for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
                 for (int gg = 0; gg < 2; ++gg) {
-                    dv[dt] = mfma32(lds_tr_operand<HD>(ot, sub * 32 + 16 * gg, 32 * dt, lane), pB[gg], dv[dt]);
-                    dk[dt] = mfma32(lds_tr_operand<HD>(qt, sub * 32 + 16 * gg, 32 * dt, lane), dsB[gg], dk[dt]);
+                    dv[dt] = mfma32(rd.tr_operand(ot, sub * 32 + 16 * gg, dt), pB[gg], dv[dt]);
+                    dk[dt] = mfma32(rd.tr_operand(qt, sub * 32 + 16 * gg, dt), dsB[gg], dk[dt]);
                 }
         }
+    };
+
+    if (total > 0) issue(0, 0);
+    for (int j = 0; j < total; ++j) {
+        wait_vmem();
+        __syncthreads();  // block j is in LDS; every wave is done with stage (j & 1) ^ 1
+        if (j + 1 < total) issue(j + 1, (j & 1) ^ 1);
+        const int q0 = (m_first + j % n_qb) * BM;
+        if (CAUSAL && q0 + BM - 1 + causal_off < kw0) continue;  // no query of the block sees these keys
+        const bool need_mask = q0 + BM > sq || kw0 + 32 > sk || (CAUSAL && kw0 + 31 > q0 + causal_off);
+        if (need_mask)
+            block(j, q0, std::true_type{});
+        else
+            block(j, q0, std::false_type{});
     }
 
     if (kv_ok) {
