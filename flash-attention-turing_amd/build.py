@@ -41,6 +41,9 @@ HIP_FLAGS = [
     f"-I{CSRC}",
 ]
 
+# Per-source additions to HIP_FLAGS (none at present).
+FILE_FLAGS = {}
+
 
 def _run(cmd):
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
@@ -59,7 +62,7 @@ def build_library(jobs: int) -> str:
 
     def compile_one(src):
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
         return obj
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:

@@ -52,7 +52,12 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a
     }
 #pragma unroll
     for (int off = KCH / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, KCH);
-    if (c == 0) a.dsum[(int64_t(b) * a.nheads + h) * a.lse_seqlen + i] = acc;
+    if (c == 0) {
+        const int64_t idx = (int64_t(b) * a.nheads + h) * a.lse_seqlen + i;
+        const int64_t plane = int64_t(a.batch) * a.nheads * a.lse_seqlen;
+        a.dsum[idx] = acc;
+        a.dsum[plane + idx] = i < si.sq ? a.lse[idx] * kLog2e : 0.f;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -119,8 +124,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         for (int t = 0; t < 8; ++t) dpart += float(ov[t]) * float(doB[g][t]);
     }
     const float dsum = dpart + __shfl_xor(dpart, 32);
-    if (qv && hh == 0) a.dsum[lrow + qi] = dsum;
     const float lse2 = qv ? a.lse[lrow + qi] * kLog2e : 0.f;
+    if (qv && hh == 0) {
+        a.dsum[lrow + qi] = dsum;
+        a.dsum[int64_t(a.batch) * a.nheads * a.lse_seqlen + lrow + qi] = lse2;  // for the dK/dV kernel
+    }
     wait_vmem();  // only the tile copies are in flight inside the loop
 
     f32x16 dq[HD / 32];
@@ -215,16 +223,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 // Needs D (dsum) from the dQ kernel or the preprocess kernel.
 template <int HD>
 struct DkvCfg {
-    static constexpr int BN = 128, BM = 64, NT = kBwdThreads;
+    static constexpr int BN = 128, NT = kBwdThreads;
+    static constexpr int BM = 64;                         // queries per block (two 32-query MFMA tiles)
     static constexpr int QTILE = BM * HD * 2;             // Q or dO tile, natural layout
     static constexpr int STAGE = 2 * QTILE + 2 * BM * 4;  // Q, dO, LSE, D
+    static constexpr int KTILE = BN * HD * 2;             // the workgroup's K (or V) rows
+    // Where the B operands live: K and V stay in LDS for the whole kernel, which
+    // leaves the register file to the dK/dV accumulators and the operand
+    // pipeline (one workgroup per CU).
+    static constexpr bool K_LDS = true, V_LDS = true;
+    static constexpr int LDS = 2 * STAGE + (K_LDS ? KTILE : 0) + (V_LDS ? KTILE : 0);
+    static constexpr int OCC = LDS <= 80 * 1024 ? 2 : 1;  // workgroups per CU
 };
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
+__global__ __launch_bounds__(256, DkvCfg<HD>::OCC) void bwd_dkdv_kernel(const fa_bwd_args a) {
     using C = DkvCfg<HD>;
     constexpr int BN = C::BN, BM = C::BM, NT = C::NT;
-    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+    __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -251,12 +267,53 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     const int kw0 = k0 + wave * 32;
     const int key = kw0 + col;
     const bool kv_ok = key < sk;
-    f16x8 kB[HD / 16], vB[HD / 16];
+    TileReader<HD> rd;
+    rd.init(lane);
+    // K, V rows of the workgroup as MFMA B operands (lane: key col, d = 16g + 8hh + 0..7),
+    // in registers or in LDS.  In LDS, row r of each 32-row group is stored at
+    // position sigma(r), so the B-operand read of key col is the conflict-free
+    // A-operand pattern.
+    char *kvs = smem + 2 * C::STAGE;
+    char *ks_lds = kvs;
+    char *vs_lds = kvs + (C::K_LDS ? C::KTILE : 0);
+    auto load_rows = [&](char *tile, const f16 *src, int64_t rs) {
+        constexpr int KCH = HD / 8;
 #pragma unroll
-    for (int g = 0; g < HD / 16; ++g) {
-        kB[g] = as_h8(kv_ok ? ldg16(kp + int64_t(key) * a.k.row_stride + 16 * g + 8 * hh) : zero_u4());
-        vB[g] = as_h8(kv_ok ? ldg16(vp + int64_t(key) * a.v.row_stride + 16 * g + 8 * hh) : zero_u4());
+        for (int i = 0; i < BN * KCH / NT; ++i) {
+            const int base = (i * (NT / 64) + wave) * 64;
+            const int p = base + lane, pos = p / KCH, cs = p % KCH;
+            const int row = (pos & ~31) | sigma(pos & 31);
+            const int64_t r = min(k0 + row, sk - 1);
+            g2l16(src + r * rs + 8 * (cs ^ swz<KCH>(pos)), tile + base * 16);
+        }
+    };
+    f16x8 kB[C::K_LDS ? 1 : HD / 16], vB[C::V_LDS ? 1 : HD / 16];
+    if constexpr (C::K_LDS) {
+        load_rows(ks_lds, kp, a.k.row_stride);
+    } else {
+#pragma unroll
+        for (int g = 0; g < HD / 16; ++g)
+            kB[g] = as_h8(kv_ok ? ldg16(kp + int64_t(key) * a.k.row_stride + 16 * g + 8 * hh) : zero_u4());
     }
+    if constexpr (C::V_LDS) {
+        load_rows(vs_lds, vp, a.v.row_stride);
+    } else {
+#pragma unroll
+        for (int g = 0; g < HD / 16; ++g)
+            vB[g] = as_h8(kv_ok ? ldg16(vp + int64_t(key) * a.v.row_stride + 16 * g + 8 * hh) : zero_u4());
+    }
+    auto k_operand = [&](int g) {
+        if constexpr (C::K_LDS)
+            return rd.a_operand(ks_lds, 32 * wave, g);
+        else
+            return kB[g];
+    };
+    auto v_operand = [&](int g) {
+        if constexpr (C::V_LDS)
+            return rd.a_operand(vs_lds, 32 * wave, g);
+        else
+            return vB[g];
+    };
     wait_vmem();  // only the tile copies are in flight inside the loop
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
@@ -270,8 +327,6 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
     const int n_qb = max(0, (sq + BM - 1) / BM - m_first);
     const int total = G * n_qb;
 
-    TileReader<HD> rd;
-    rd.init(lane);
     TileCopier<HD, BM, NT> qcp, ocp;
     qcp.init(qrs, wave, lane);
     ocp.init(dors, wave, lane);
@@ -292,9 +347,16 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
             dma_tile<HD, BM, NT>(qt, qp, qrs, q0, sq - 1, wave, lane);
             dma_tile<HD, BM, NT>(ot, dop, dors, q0, sq - 1, wave, lane);
         }
-        const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
-        if (wave == 0) g2l4(a.lse + lrow, lf);
-        if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
+        // LSE*log2(e) (second plane of the dsum workspace) and D per query row.
+        const float *lse2 = a.dsum + int64_t(a.batch) * a.nheads * a.lse_seqlen;
+        if constexpr (BM == 64) {
+            const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
+            if (wave == 0) g2l4(lse2 + lrow, lf);
+            if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
+        } else {  // lanes 0..31: LSE rows, lanes 32..63: D rows
+            const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + (lane & 31), sq - 1);
+            if (wave == 0) g2l4((lane < 32 ? lse2 : a.dsum) + lrow, lf);
+        }
     };
 
     // One (q-head, query block): S = Q K^T and dP = dO V^T per 32-query half,
@@ -306,13 +368,16 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
         const char *ot = qt + C::QTILE;
         const float *lf = reinterpret_cast<const float *>(ot + C::QTILE);
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {  // 32-query halves of the block
-            f32x16 s = mfma32(rd.a_operand(qt, 32 * sub, 0), kB[0], zero16());
-            f32x16 dp = mfma32(rd.a_operand(ot, 32 * sub, 0), vB[0], zero16());
+        for (int sub = 0; sub < BM / 32; ++sub) {  // 32-query tiles of the block
+            // Scheduling fences keep each phase's operand reads local, so the
+            // dK/dV accumulators and the S/dP tiles fit the register file.
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16 s = mfma32(rd.a_operand(qt, 32 * sub, 0), k_operand(0), zero16());
+            f32x16 dp = mfma32(rd.a_operand(ot, 32 * sub, 0), v_operand(0), zero16());
 #pragma unroll
             for (int g = 1; g < HD / 16; ++g) {
-                s = mfma32(rd.a_operand(qt, 32 * sub, g), kB[g], s);
-                dp = mfma32(rd.a_operand(ot, 32 * sub, g), vB[g], dp);
+                s = mfma32(rd.a_operand(qt, 32 * sub, g), k_operand(g), s);
+                dp = mfma32(rd.a_operand(ot, 32 * sub, g), v_operand(g), dp);
             }
 #pragma unroll
             for (int r8 = 0; r8 < 2; ++r8) {
@@ -324,7 +389,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const int r = 8 * r8 + u;
-                    const float l2 = (u < 4 ? l_a[u] : l_b[u - 4]) * kLog2e;
+                    const float l2 = u < 4 ? l_a[u] : l_b[u - 4];
                     const float dsum = u < 4 ? d_a[u] : d_b[u - 4];
                     float p = exp2_fast(fmaf(s[r], cs, -l2));
                     if constexpr (MASK) {
@@ -336,6 +401,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const fa_bwd_args a) {
                     dp[r] = p * (dp[r] - dsum);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
             f16x8 pB[2], dsB[2];
 #pragma unroll
             for (int gg = 0; gg < 2; ++gg) {

@@ -137,7 +137,7 @@ std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Te
     at::Tensor dq = at::empty(q.sizes(), q.options());
     at::Tensor dk = at::empty(k.sizes(), k.options());
     at::Tensor dv = at::empty(v.sizes(), v.options());
-    at::Tensor dsum = at::empty(l.sizes(), l.options());
+    at::Tensor dsum = at::empty({2, l.numel()}, l.options());  // D, then LSE*log2(e)
 
     fa_bwd_args a{};
     a.q = desc4(q);
@@ -256,7 +256,7 @@ std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v,
     at::Tensor dq = at::zeros(q.sizes(), q.options());
     at::Tensor dk = at::zeros(k.sizes(), k.options());
     at::Tensor dv = at::zeros(v.sizes(), v.options());
-    at::Tensor dsum = at::empty(l.sizes(), l.options());
+    at::Tensor dsum = at::empty({2, l.numel()}, l.options());  // D, then LSE*log2(e)
 
     fa_bwd_args a{};
     a.q = desc3(q);
