@@ -177,9 +177,10 @@ def decode_setup(device, seed=3):
     lse = torch.empty((b, h, 1), dtype=torch.float32, device=device)
     rows = b * h
     ws = torch.empty(splits * rows * (d + 1), dtype=torch.float32, device=device)
+    order = torch.empty(b, dtype=torch.int32, device=device)
     args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, seqlens, d ** -0.5, True, splits, k_new=k_new,
                                 v_new=v_new, block_table=table_d, out_accum=ws[: splits * rows * d],
-                                lse_accum=ws[splits * rows * d :])
+                                lse_accum=ws[splits * rows * d :], batch_order=order)
     launches = [
         ("kv_append", lambda: fa_capi.call("fa_kv_append", args)),
         ("kv_splitkv", lambda: fa_capi.call("fa_kv_splitkv", args)),

@@ -152,6 +152,8 @@ __device__ __forceinline__ void g2l4(const void *g, char *lds_base) {
 
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt lgkmcnt(0): every LDS read issued so far has returned its data.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // s_waitcnt vmcnt(N), N < 64.
 template <int N>
 __device__ __forceinline__ void wait_vmem_n() {

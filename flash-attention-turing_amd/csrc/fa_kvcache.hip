@@ -82,14 +82,19 @@ struct KvCfg {
     static constexpr int KCH = HD / 8;
     static constexpr int TILE = kTile * HD * 2;         // one K or V tile, natural layout
     static constexpr int STAGE = 2 * TILE;              // K tile, then V tile
-    static constexpr int NST = 2;                       // ring stages per wave
+    // Ring stages per wave.  One stage suffices: a tile's operands are read
+    // into registers and the stage is refilled before the tile is computed,
+    // and the smaller footprint lets two workgroups share a CU (one's start-up
+    // and merge overlap the other's streaming).
+    static constexpr int NST = 1;
     static constexpr int WAVE_LDS = NST * STAGE;        // also holds HD x 32 fp32 at the merge
     static constexpr int CPW = kTile * KCH / 64;        // copies per lane per tile (K or V)
     static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
 };
 
 template <int HD>
-__global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a, const int row_tiles) {
+__global__ __launch_bounds__(256, KvCfg<HD>::NST == 1 ? 2 : 1) void kv_splitkv_kernel(const fa_kvcache_args a,
+                                                                                   const int row_tiles) {
     using C = KvCfg<HD>;
     __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
     __shared__ int pages[C::MAX_PAGES];
@@ -97,12 +102,17 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int col = lane & 31, hh = lane >> 5;
-    const int split = blockIdx.y;
+    // One-dimensional grid, sequence rank slowest: with batch_order the
+    // longest sequences' workgroups are dispatched first (longest-job-first
+    // keeps the last wave of workgroups short).
     int rest = blockIdx.x;
     const int rt = rest % row_tiles;
     rest /= row_tiles;
     const int hk = rest % a.nheads_k;
-    const int b = rest / a.nheads_k;
+    rest /= a.nheads_k;
+    const int split = rest % a.num_splits;
+    const int rank = rest / a.num_splits;
+    const int b = a.batch_order ? a.batch_order[rank] : rank;
     const int G = a.nheads / a.nheads_k;
     const int R = G * a.seqlen_q;  // rows of this (batch, kv head): row = qpos * G + g
 
@@ -187,20 +197,33 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
         dma_tile<HD, kTile, 64>(vs, vb, vrs, 0, L - 1 - p0, 0, lane);
     };
 
+    TileReader<HD> rd;
+    rd.init(lane);
     if (n_my > 0) issue(my_first, 0);
-    if (n_my > 1) issue(my_first + kKvWaves, 1);
+    if (C::NST > 1 && n_my > 1) issue(my_first + kKvWaves, 1);
     for (int k = 0; k < n_my; ++k) {
-        const int st = k & 1;
+        const int st = k % C::NST;
         if (k + 1 < n_my)
-            wait_vmem_n<2 * C::CPW>();  // the newer tile may stay in flight
+            wait_vmem_n<(C::NST - 1) * 2 * C::CPW>();  // newer tiles may stay in flight
         else
             wait_vmem();
         const char *ks = smem + (wave * C::NST + st) * C::STAGE;
         const char *vs = ks + C::TILE;
         const int p0 = (my_first + k * kKvWaves) * kTile;
-        f32x16 s = zero16();
+        // All operands of the tile into registers first, then refill the stage
+        // right away: two tiles stay in flight while this one is computed.
+        f16x8 ka[HD / 16], va[HD / 32][2];
 #pragma unroll
-        for (int g = 0; g < HD / 16; ++g) s = mfma32(lds_ld16(ks, tile_off<HD>(sigma(col), 2 * g + hh)), qB[g], s);
+        for (int g = 0; g < HD / 16; ++g) ka[g] = rd.a_operand(ks, 0, g);
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) va[dt][gg] = rd.tr_operand(vs, 16 * gg, dt);
+        wait_lds();
+        if (k + C::NST < n_my) issue(my_first + (k + C::NST) * kKvWaves, st);
+        f32x16 s = mfma32(ka[0], qB[0], zero16());
+#pragma unroll
+        for (int g = 1; g < HD / 16; ++g) s = mfma32(ka[g], qB[g], s);
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -239,14 +262,10 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
             for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
 #pragma unroll
             for (int gg = 0; gg < 2; ++gg) {
-                const f16x8 va = lds_tr_operand<HD>(vs, 16 * gg, 32 * dt, lane);
-                o[dt] = mfma32(va, ph[gg], o[dt]);
-                o[dt] = mfma32(va, pl[gg], o[dt]);
+                o[dt] = mfma32(va[dt][gg], ph[gg], o[dt]);
+                o[dt] = mfma32(va[dt][gg], pl[gg], o[dt]);
             }
         }
-        // Stage st is free again (every read above has been consumed): refill it.
-        __builtin_amdgcn_wave_barrier();
-        if (k + 2 < n_my) issue(my_first + (k + 2) * kKvWaves, st);
     }
     };
     if (pages_in_lds)
@@ -302,6 +321,21 @@ __global__ __launch_bounds__(256) void kv_splitkv_kernel(const fa_kvcache_args a
             a.out_accum[(int64_t(split) * nrow_all + orow) * HD + d] = outv;
             if (d == 0) a.lse_accum[int64_t(split) * nrow_all + orow] = lse;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// batch_order[r] = the sequence with the r-th largest key count (ties by index).
+constexpr int kOrderMaxBatch = 2048;
+__global__ __launch_bounds__(256) void kv_order_kernel(const fa_kvcache_args a) {
+    __shared__ int lens[kOrderMaxBatch];
+    for (int i = threadIdx.x; i < a.batch; i += 256) lens[i] = a.cache_seqlens[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.batch; i += 256) {
+        const int li = lens[i];
+        int rank = 0;
+        for (int j = 0; j < a.batch; ++j) rank += (lens[j] > li) || (lens[j] == li && j < i);
+        a.batch_order[rank] = i;
     }
 }
 
@@ -401,15 +435,22 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     if (a.num_splits > 1 && (!a.out_accum || !a.lse_accum)) return FA_ERR_WORKSPACE;
     const int R = (a.nheads / a.nheads_k) * a.seqlen_q;
     const int row_tiles = (R + 31) / 32;
-    const int64_t gx = int64_t(a.batch) * a.nheads_k * row_tiles;
+    const int64_t gx = int64_t(a.batch) * a.nheads_k * row_tiles * a.num_splits;
     if (gx == 0) return FA_OK;
-    if (gx > 0x7fffffff || a.num_splits > 65535) return FA_ERR_INVALID_ARG;
+    if (gx > 0x7fffffff) return FA_ERR_INVALID_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid(unsigned(gx), unsigned(a.num_splits));
+    fa_kvcache_args run = a;
+    if (a.batch_order && a.batch > 1 && a.batch <= fa::kOrderMaxBatch) {
+        hipLaunchKernelGGL(fa::kv_order_kernel, dim3(1), dim3(256), 0, s, a);
+        const int rc = int(hipGetLastError());
+        if (rc) return rc;
+    } else {
+        run.batch_order = nullptr;  // natural order
+    }
     if (a.head_dim == 128)
-        hipLaunchKernelGGL(fa::kv_splitkv_kernel<128>, grid, dim3(fa::kKvThreads), 0, s, a, row_tiles);
+        hipLaunchKernelGGL(fa::kv_splitkv_kernel<128>, dim3(unsigned(gx)), dim3(fa::kKvThreads), 0, s, run, row_tiles);
     else
-        hipLaunchKernelGGL(fa::kv_splitkv_kernel<64>, grid, dim3(fa::kKvThreads), 0, s, a, row_tiles);
+        hipLaunchKernelGGL(fa::kv_splitkv_kernel<64>, dim3(unsigned(gx)), dim3(fa::kKvThreads), 0, s, run, row_tiles);
     return int(hipGetLastError());
 }
 

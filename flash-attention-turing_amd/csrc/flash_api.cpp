@@ -441,13 +441,16 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
         a.num_splits = fa_kv_num_splits(num_splits, int(seqlen_cache), int(head_size), int(seqlen_q),
                                         int(batch_size), int(num_heads), int(num_heads_k),
                                         num_cus(q.get_device()));
-        at::Tensor ws;
+        // Workspace: split accumulators (num_splits > 1), then the longest-first
+        // sequence order the split kernel schedules by.
+        const int64_t rows = batch_size * num_heads * seqlen_q;
+        const int64_t acc_floats = a.num_splits > 1 ? a.num_splits * rows * (head_size + 1) : 0;
+        at::Tensor ws = at::empty({acc_floats + batch_size}, q.options().dtype(at::kFloat));
         if (a.num_splits > 1) {
-            const int64_t rows = batch_size * num_heads * seqlen_q;
-            ws = at::empty({a.num_splits * rows * (head_size + 1)}, q.options().dtype(at::kFloat));
             a.out_accum = ws.data_ptr<float>();
             a.lse_accum = a.out_accum + a.num_splits * rows * head_size;
         }
+        a.batch_order = reinterpret_cast<int32_t *>(ws.data_ptr<float>() + acc_floats);
         check_rc(fa_kv_splitkv(&a, stream), "fa_kv_splitkv");
         check_rc(fa_kv_combine(&a, stream), "fa_kv_combine");
         return {out, lse};

@@ -60,7 +60,7 @@ class FaKvcacheArgs(ctypes.Structure):
         ("block_table_stride", _i64),
         ("batch", _i32), ("seqlen_q", _i32), ("nheads", _i32), ("nheads_k", _i32), ("head_dim", _i32),
         ("seqlen_new", _i32), ("page_block_size", _i32), ("num_splits", _i32), ("softmax_scale", _f32),
-        ("causal", _i32), ("out_accum", _p), ("lse_accum", _p),
+        ("causal", _i32), ("out_accum", _p), ("lse_accum", _p), ("batch_order", _p),
     ]
 
 
@@ -176,7 +176,7 @@ def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, caus
 
 def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: float, causal: bool, num_splits: int,
                  k_new=None, v_new=None, cache_batch_idx=None, block_table=None, out_accum=None,
-                 lse_accum=None) -> FaKvcacheArgs:
+                 lse_accum=None, batch_order=None) -> FaKvcacheArgs:
     a = FaKvcacheArgs()
     a.q, a.k_cache, a.v_cache, a.o = (tensor_desc(x) for x in (q, k_cache, v_cache, o))
     a.k_new, a.v_new = tensor_desc(k_new), tensor_desc(v_new)
@@ -191,4 +191,5 @@ def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: floa
     a.softmax_scale = softmax_scale
     a.causal = int(causal)
     a.out_accum, a.lse_accum = ptr(out_accum), ptr(lse_accum)
+    a.batch_order = ptr(batch_order)
     return a

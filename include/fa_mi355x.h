@@ -120,13 +120,16 @@ typedef struct fa_kvcache_args {
     int32_t causal;
     float *out_accum;               /* workspace [num_splits][batch*nheads*seqlen_q][d] fp32 */
     float *lse_accum;               /* workspace [num_splits][batch*nheads*seqlen_q] fp32    */
+    int32_t *batch_order;           /* workspace [batch]: sequences longest first (filled by
+                                       fa_kv_splitkv), or NULL for the natural order           */
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);
  * requested > 0 is returned unchanged. */
 int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seqlen_q,
                      int batch, int nheads, int nheads_k, int num_cus);
-/* Workspace bytes fa_kv_splitkv needs for args->num_splits (0 when num_splits == 1). */
+/* Bytes of the split accumulators for args->num_splits (0 when num_splits == 1);
+ * batch_order, when used, needs batch * 4 more. */
 size_t fa_kv_workspace_bytes(const fa_kvcache_args *args);
 /* In-place append of k_new/v_new at cache_seqlens (contiguous, remapped or paged). */
 int fa_kv_append(const fa_kvcache_args *args, void *stream);
