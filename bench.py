@@ -11,8 +11,10 @@ inputs already resident in HBM:
   computes the dO.O row sums; fa_bwd_dkdv) into preallocated outputs.  ``value`` is the
   algorithmic TFLOPS of the step: (4 + 10) * b * h * d * pairs / step time.
 * extra, reported in the same line: the same step at seqlen 8192 (seed 5, the
-  point the 50 % / 35 % MFMA targets are quoted on) and the paged split-KV
-  decode with append (config c4, seed 3) in HBM GB/s.
+  point the 50 % / 35 % MFMA targets are quoted on), the packed varlen GQA
+  step (config c3, seed 2), the paged split-KV decode with append (config c4,
+  seed 3) and the long-context remapped-cache decode (config c5, seed 4), the
+  last two in HBM GB/s.  ``--no-8k`` keeps only the headline shapes (c2, c4).
 
 Per-kernel durations come from HIP events recorded on the launch stream
 between the launches of the timed region.  The CPU baseline is PyTorch's CPU
@@ -44,10 +46,10 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 # (FETCH x 2.0, WRITE x 1.0); summary in profiles/hbm_bytes_pmc_c2_c4.md.
 # Re-measured whenever a kernel changes; None where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 6.694e8 + 6.82e7,
-    "bwd_dq": 7.445e8 + 6.72e7,
-    "bwd_dkdv": 7.406e8 + 1.827e8,
-    "kv_splitkv": 4.699e9 + 8.5e6,
+    "fwd": 6.801e8 + 6.816e7,
+    "bwd_dq": 6.148e8 + 7.350e7,
+    "bwd_dkdv": 7.397e8 + 1.645e8,
+    "kv_splitkv": 4.693e9 + 8.52e6,
 }
 
 
@@ -197,6 +199,79 @@ def decode_setup(device, seed=3):
     return launches, info, dict(out=out, lse=lse)
 
 
+def varlen_setup(device, seed=2):
+    """Config c3: 16 packed causal sequences, lengths U[128, 4096], 32 q / 8 kv heads, d128."""
+    import torch
+
+    import fa_capi
+
+    h, hk, d = 32, 8, 128
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(128, 4097, (16,), generator=g)
+    cu = torch.zeros(17, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    total, mx = int(cu[-1]), int(lens.max())
+    q = seeded_fp16((total, h, d), g, device)
+    k = seeded_fp16((total, hk, d), g, device)
+    v = seeded_fp16((total, hk, d), g, device)
+    do = seeded_fp16((total, h, d), g, device)
+    cu_d = cu.to(device)
+    o = torch.empty_like(q)
+    lse = torch.empty((16, h, mx), dtype=torch.float32, device=device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=device)
+    scale = d ** -0.5
+    fa = fa_capi.fwd_args(q, k, v, o, lse, scale, True, cu_d, cu_d, mx, mx)
+    ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, True, cu_d, cu_d, mx, mx)
+    launches = [
+        ("fwd", lambda: fa_capi.call("fa_fwd", fa)),
+        ("bwd_dq", lambda: fa_capi.call("fa_bwd_dq", ba)),
+        ("bwd_dkdv", lambda: fa_capi.call("fa_bwd_dkdv", ba)),
+    ]
+    unit = h * d * sum(int(n) * (int(n) + 1) // 2 for n in lens)
+    info = {"sequences": 16, "total_tokens": total, "max_seqlen": mx, "heads": h, "heads_k": hk, "head_dim": d}
+    return launches, info, unit, dict(o=o, dq=dq, dk=dk, dv=dv)
+
+
+def longctx_setup(device, seed=4):
+    """Config c5: contiguous cache 8 x 131072, 16 heads, d64; batch 4 rows remapped by
+    cache_batch_idx, 4 query tokens appended and attended causally, 16 splits."""
+    import torch
+
+    import fa_capi
+
+    rows, cap, h, d, b, sq, splits = 8, 131072, 16, 64, 4, 4, 16
+    g = torch.Generator().manual_seed(seed)
+    batch_idx = torch.randperm(rows, generator=g)[:b].to(torch.int32)
+    lens = torch.randint(65536, 131069, (b,), generator=g)
+    gd = torch.Generator(device=device).manual_seed(seed)
+    k_cache = torch.randn((rows, cap, h, d), generator=gd, device=device, dtype=torch.float16)
+    v_cache = torch.randn((rows, cap, h, d), generator=gd, device=device, dtype=torch.float16)
+    q = seeded_fp16((b, sq, h, d), g, device)
+    k_new = seeded_fp16((b, sq, h, d), g, device)
+    v_new = seeded_fp16((b, sq, h, d), g, device)
+    out = torch.empty_like(q)
+    lse = torch.empty((b, h, sq), dtype=torch.float32, device=device)
+    nrow = b * h * sq
+    ws = torch.empty(splits * nrow * (d + 1), dtype=torch.float32, device=device)
+    order = torch.empty(b, dtype=torch.int32, device=device)
+    args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, lens.to(torch.int32).to(device), d ** -0.5, True,
+                                splits, k_new=k_new, v_new=v_new, cache_batch_idx=batch_idx.to(device),
+                                out_accum=ws[: splits * nrow * d], lse_accum=ws[splits * nrow * d :],
+                                batch_order=order)
+    launches = [
+        ("kv_append", lambda: fa_capi.call("fa_kv_append", args)),
+        ("kv_splitkv", lambda: fa_capi.call("fa_kv_splitkv", args)),
+        ("kv_combine", lambda: fa_capi.call("fa_kv_combine", args)),
+    ]
+    ends = lens + sq
+    kv_bytes = int(ends.sum()) * h * d * 2 * 2
+    other = 2 * b * sq * h * d * 2 + 2 * 2 * b * sq * h * d * 2 + nrow * 4 + 2 * b * 4
+    info = {"cache_rows": rows, "capacity": cap, "batch": b, "seqlen_q": sq, "heads": h, "head_dim": d,
+            "num_splits": splits, "tokens": int(ends.sum()), "kv_bytes": kv_bytes, "bytes": kv_bytes + other}
+    return launches, info, dict(out=out)
+
+
 def cpu_baseline_train(tensors, hd):
     """CPU SDPA fwd + bwd (fp32, causal) on batch 1 of the headline inputs."""
     import torch
@@ -248,7 +323,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "train", "decode", "copy"], default="all",
                     help="copy: a plain 1 GiB device copy, the calibration kernel for HBM byte counters")
-    ap.add_argument("--no-8k", action="store_true", help="omit the seqlen 8192 point")
+    ap.add_argument("--no-8k", action="store_true",
+                    help="headline shapes only: omit the seqlen 8192 point and the c3 / c5 configurations")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (collectives, sharding) "
@@ -311,6 +387,25 @@ def main():
             del launches, tensors
             torch.cuda.empty_cache()
 
+    if args.only in ("all", "train") and not args.no_8k:
+        log("varlen c3: 16 causal sequences, GQA 32/8, d128 (seed 2)")
+        launches, info, unit, outs = varlen_setup(device)
+        ms_v, perv = Timed(launches).run(max(3, args.steps // 2), max(1, args.warmup // 2))
+        for name, t in outs.items():
+            assert torch.isfinite(t).all(), f"non-finite varlen {name}"
+        flops = {"fwd": 4 * unit, "bwd_dq": 6 * unit, "bwd_dkdv": 8 * unit}
+        bwd_ms = perv["bwd_dq"] + perv["bwd_dkdv"]
+        info.update(
+            ms_per_step=round(ms_v, 4),
+            kernels={n: {"ms": round(ms, 4), "tflops": round(flops[n] / (ms * 1e-3) / 1e12, 1)} for n, ms in perv.items()},
+            fwd_tflops=round(4 * unit / (perv["fwd"] * 1e-3) / 1e12, 1),
+            bwd_tflops=round(10 * unit / (bwd_ms * 1e-3) / 1e12, 1),
+        )
+        result["varlen_c3"] = info
+        log(f"varlen: {info}")
+        del launches, outs
+        torch.cuda.empty_cache()
+
     if args.only in ("all", "decode"):
         log("decode c4: paged split-KV with append (seed 3)")
         launches, info, outs = decode_setup(device)
@@ -326,6 +421,22 @@ def main():
         info["frac_hbm_peak"] = round(info["gbs_call"] / PEAK_HBM_GBS, 4)
         result["decode_c4"] = info
         log(f"decode: {info}")
+        del launches, outs
+        torch.cuda.empty_cache()
+        if not args.no_8k:
+            log("long-context c5: contiguous 8 x 131072 cache, remapped rows, 4-token append, 16 splits (seed 4)")
+            launches5, info5, outs5 = longctx_setup(device)
+            ms5, per5 = Timed(launches5).run(args.steps, args.warmup)
+            assert torch.isfinite(outs5["out"]).all(), "non-finite long-context output"
+            t5 = sum(per5.values())
+            info5.update(ms_per_call=round(ms5, 4), kernels_ms={k: round(v, 4) for k, v in per5.items()},
+                         gbs_call=round(info5["bytes"] / (t5 * 1e-3) / 1e9, 1),
+                         gbs_splitkv=round(info5["kv_bytes"] / (per5["kv_splitkv"] * 1e-3) / 1e9, 1))
+            info5["frac_hbm_peak"] = round(info5["gbs_call"] / PEAK_HBM_GBS, 4)
+            result["longctx_c5"] = info5
+            log(f"long-context: {info5}")
+            del launches5, outs5
+            torch.cuda.empty_cache()
         if args.only == "decode":
             result.update(metric="paged split-KV decode HBM GB/s", value=info["gbs_call"], unit="GB/s",
                           ms_per_step=info["ms_per_call"],

@@ -16,14 +16,20 @@
 // K/V byte of the split is read once.  The keys of the split are walked in
 // 32-key tiles aligned to absolute positions (a tile never straddles a page:
 // pages are multiples of 256 tokens), tile t going to wave t % 4.  Each wave
-// streams its tiles through a private two-stage LDS ring with direct
-// global -> LDS copies (global_load_lds): while one tile is computed the next
-// one is in flight, with no register staging and no workgroup barrier in the
-// loop.  K stays natural (MFMA A operand rows), V natural and read transposed
-// with ds_read_b64_tr_b16.  Each wave keeps its own online softmax state; the
-// four waves merge their partial states through LDS at the end.  Paged,
-// remapped and contiguous caches take the same tile order and the same
-// arithmetic, so their results are bit-identical for the same logical cache.
+// streams its tiles through a private LDS slot with direct global -> LDS
+// copies (global_load_lds): it reads a tile's MFMA operands into registers,
+// issues the next tile's copy into the same slot and then computes, so the
+// copy is in flight during the compute, with no register staging of the copy
+// and no workgroup barrier in the loop.  K stays natural (MFMA A operand
+// rows), V natural and read transposed with ds_read_b64_tr_b16.  Each wave
+// keeps its own online softmax state; the four waves merge their partial
+// states through LDS at the end.  Paged, remapped and contiguous caches take
+// the same tile order and the same arithmetic, so their results are
+// bit-identical for the same logical cache.  The grid is 1-D with the
+// sequence rank slowest: when the caller passes a batch_order workspace, a
+// one-workgroup kernel first ranks the sequences by key count (longest
+// first), so the longest sequences start first and the short ones fill the
+// tail of the launch.
 #include <algorithm>
 #include <type_traits>
 

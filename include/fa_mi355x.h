@@ -92,7 +92,7 @@ int fa_bwd_dq(const fa_bwd_args *args, void *stream);
 /* dK/dV kernel with in-kernel GQA accumulation (flash_bwd_kernel.h:613-1344); reads the
  * dsum workspace written by fa_bwd_dq or fa_bwd_preprocess. */
 int fa_bwd_dkdv(const fa_bwd_args *args, void *stream);
-/* preprocess + dQ + dK/dV in stream order. */
+/* dQ (with the dsum workspace) then dK/dV, in stream order. */
 int fa_bwd(const fa_bwd_args *args, void *stream);
 
 /*
