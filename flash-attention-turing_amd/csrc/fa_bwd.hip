@@ -214,36 +214,41 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV kernel: 4 waves x 32 keys of one (batch, KV head); K, V stay in
-// registers as B operands.  For every q-head of the GQA group and every
-// 64-query block that sees these keys, Q, dO, LSE and D are copied HBM -> LDS
-// (two stages); S = Q K^T and dP = dO V^T read Q, dO as natural A operands,
-// dV^T += dO^T P and dK^T += Q^T dS read them transposed.  The group's
-// contributions accumulate in fp32 registers (no per-q-head dK/dV buffers).
-// Needs D (dsum) from the dQ kernel or the preprocess kernel.
+// dK/dV kernel: 8 waves over 128 keys of one (batch, KV head).  Wave w owns
+// keys 32 (w % 4) .. +31 and, of every 64-query block, the 32-query half
+// w / 4, so two waves share each SIMD and the register file holds one 32 x 32
+// S / dP tile per wave next to its dK/dV accumulators.  K and V stay in LDS
+// for the whole kernel as MFMA B operands.  For every q-head of the GQA group
+// and every query block that sees these keys, Q, dO, LSE and D are copied
+// HBM -> LDS (two stages); S = Q K^T and dP = dO V^T read Q, dO as natural A
+// operands, dV^T += dO^T P and dK^T += Q^T dS read them transposed.  The
+// group's contributions accumulate in fp32 registers (no per-q-head dK/dV
+// buffers); at the end the two waves of a key range add their partial sums
+// through LDS, one wave finishing dK and the other dV.  Needs D and
+// LSE*log2(e) (the dsum workspace) from the dQ or the preprocess kernel.
+constexpr int kDkvThreads = 512;
+
 template <int HD>
 struct DkvCfg {
-    static constexpr int BN = 128, NT = kBwdThreads;
-    static constexpr int BM = 64;                         // queries per block (two 32-query MFMA tiles)
+    static constexpr int BN = 128, NT = kDkvThreads;
+    static constexpr int BM = 64;                         // queries per block (one 32-query half per wave)
     static constexpr int QTILE = BM * HD * 2;             // Q or dO tile, natural layout
     static constexpr int STAGE = 2 * QTILE + 2 * BM * 4;  // Q, dO, LSE, D
     static constexpr int KTILE = BN * HD * 2;             // the workgroup's K (or V) rows
-    // Where the B operands live: K and V stay in LDS for the whole kernel, which
-    // leaves the register file to the dK/dV accumulators and the operand
-    // pipeline (one workgroup per CU).
-    static constexpr bool K_LDS = true, V_LDS = true;
-    static constexpr int LDS = 2 * STAGE + (K_LDS ? KTILE : 0) + (V_LDS ? KTILE : 0);
-    static constexpr int OCC = LDS <= 80 * 1024 ? 2 : 1;  // workgroups per CU
+    static constexpr int LDS = 2 * STAGE + 2 * KTILE;
+    static constexpr int XCH = 2 * BN * HD * 4;           // dK and dV partials handed between waves
+    static_assert(XCH <= LDS, "partial-sum exchange reuses the tiles' LDS");
 };
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, DkvCfg<HD>::OCC) void bwd_dkdv_kernel(const fa_bwd_args a) {
+__global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_args a) {
     using C = DkvCfg<HD>;
     constexpr int BN = C::BN, BM = C::BM, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int kg = wave & 3, half = wave >> 2;                  // key group, query half
     const int col = lane & 31, hh = lane >> 5;
     const int bh_count = a.batch * a.nheads_k;
     const int bhk = blockIdx.x % bh_count;
@@ -258,24 +263,21 @@ __global__ __launch_bounds__(256, DkvCfg<HD>::OCC) void bwd_dkdv_kernel(const fa
 
     const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, b, si.k_start, hk);
     const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, b, si.k_start, hk);
-    f16 *dkp = (f16 *)a.dk.ptr + base_off(a.dk, packed_k, b, si.k_start, hk);
-    f16 *dvp = (f16 *)a.dv.ptr + base_off(a.dv, packed_k, b, si.k_start, hk);
     const int causal_off = sk - sq;
     const float cs = a.softmax_scale * kLog2e;
     const int64_t qrs = a.q.row_stride, dors = a.dout.row_stride;
 
-    const int kw0 = k0 + wave * 32;
+    const int kw0 = k0 + kg * 32;
     const int key = kw0 + col;
     const bool kv_ok = key < sk;
-    TileReader<HD> rd;
-    rd.init(lane);
-    // K, V rows of the workgroup as MFMA B operands (lane: key col, d = 16g + 8hh + 0..7),
-    // in registers or in LDS.  In LDS, row r of each 32-row group is stored at
-    // position sigma(r), so the B-operand read of key col is the conflict-free
-    // A-operand pattern.
-    char *kvs = smem + 2 * C::STAGE;
-    char *ks_lds = kvs;
-    char *vs_lds = kvs + (C::K_LDS ? C::KTILE : 0);
+    TileReader<HD> rd0;
+    rd0.init(lane);
+    // K, V rows of the workgroup as MFMA B operands (lane: key col,
+    // d = 16g + 8hh + 0..7).  Row r of each 32-row group is stored at position
+    // sigma(r), so the B-operand read of key col is the conflict-free A-operand
+    // pattern.
+    char *ks_lds = smem + 2 * C::STAGE;
+    char *vs_lds = ks_lds + C::KTILE;
     auto load_rows = [&](char *tile, const f16 *src, int64_t rs) {
         constexpr int KCH = HD / 8;
 #pragma unroll
@@ -287,33 +289,8 @@ __global__ __launch_bounds__(256, DkvCfg<HD>::OCC) void bwd_dkdv_kernel(const fa
             g2l16(src + r * rs + 8 * (cs ^ swz<KCH>(pos)), tile + base * 16);
         }
     };
-    f16x8 kB[C::K_LDS ? 1 : HD / 16], vB[C::V_LDS ? 1 : HD / 16];
-    if constexpr (C::K_LDS) {
-        load_rows(ks_lds, kp, a.k.row_stride);
-    } else {
-#pragma unroll
-        for (int g = 0; g < HD / 16; ++g)
-            kB[g] = as_h8(kv_ok ? ldg16(kp + int64_t(key) * a.k.row_stride + 16 * g + 8 * hh) : zero_u4());
-    }
-    if constexpr (C::V_LDS) {
-        load_rows(vs_lds, vp, a.v.row_stride);
-    } else {
-#pragma unroll
-        for (int g = 0; g < HD / 16; ++g)
-            vB[g] = as_h8(kv_ok ? ldg16(vp + int64_t(key) * a.v.row_stride + 16 * g + 8 * hh) : zero_u4());
-    }
-    auto k_operand = [&](int g) {
-        if constexpr (C::K_LDS)
-            return rd.a_operand(ks_lds, 32 * wave, g);
-        else
-            return kB[g];
-    };
-    auto v_operand = [&](int g) {
-        if constexpr (C::V_LDS)
-            return rd.a_operand(vs_lds, 32 * wave, g);
-        else
-            return vB[g];
-    };
+    load_rows(ks_lds, kp, a.k.row_stride);
+    load_rows(vs_lds, vp, a.v.row_stride);
     wait_vmem();  // only the tile copies are in flight inside the loop
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
@@ -349,106 +326,157 @@ __global__ __launch_bounds__(256, DkvCfg<HD>::OCC) void bwd_dkdv_kernel(const fa
         }
         // LSE*log2(e) (second plane of the dsum workspace) and D per query row.
         const float *lse2 = a.dsum + int64_t(a.batch) * a.nheads * a.lse_seqlen;
-        if constexpr (BM == 64) {
-            const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
-            if (wave == 0) g2l4(lse2 + lrow, lf);
-            if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
-        } else {  // lanes 0..31: LSE rows, lanes 32..63: D rows
-            const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + (lane & 31), sq - 1);
-            if (wave == 0) g2l4((lane < 32 ? lse2 : a.dsum) + lrow, lf);
-        }
+        const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
+        if (wave == 0) g2l4(lse2 + lrow, lf);
+        if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
     };
 
-    // One (q-head, query block): S = Q K^T and dP = dO V^T per 32-query half,
-    // P, dS, then dV^T += dO^T P and dK^T += Q^T dS.
-    auto block = [&](int j, int q0, auto mask_tag) {
+    // The wave's 32-query half of block j: S = Q K^T and dP = dO V^T, P, dS,
+    // then dV^T += dO^T P and dK^T += Q^T dS.
+    auto block = [&](int j, int qh0, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const int buf = j & 1;
-        const char *qt = smem + buf * C::STAGE;
+        const char *qt = smem + (j & 1) * C::STAGE;
         const char *ot = qt + C::QTILE;
         const float *lf = reinterpret_cast<const float *>(ot + C::QTILE);
+        const int r0 = 32 * half;
+        // The per-read LDS addresses are recomputed here from an opaque copy of
+        // the lane's base offsets: hoisted out of the loop they would hold
+        // dozens of registers for the whole kernel.
+        TileReader<HD> rd = rd0;
+        asm volatile("" : "+v"(rd.a_base), "+v"(rd.tr_base[0]), "+v"(rd.tr_base[1]));
+        // Operand reads run PIPE steps ahead of the MFMAs that use them, and a
+        // scheduling fence after each step keeps that order, so the dK/dV
+        // accumulators, the S/dP tiles and the operands in flight fit the
+        // 256 registers of a two-waves-per-SIMD wave.
+        constexpr int PIPE = 2, NG = HD / 16;
+        f16x8 qa[PIPE], ka[PIPE], oa[PIPE], va[PIPE];
+        auto ld = [&](int g) {
+            qa[g % PIPE] = rd.a_operand(qt, r0, g);
+            ka[g % PIPE] = rd.a_operand(ks_lds, 32 * kg, g);
+            oa[g % PIPE] = rd.a_operand(ot, r0, g);
+            va[g % PIPE] = rd.a_operand(vs_lds, 32 * kg, g);
+        };
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int sub = 0; sub < BM / 32; ++sub) {  // 32-query tiles of the block
-            // Scheduling fences keep each phase's operand reads local, so the
-            // dK/dV accumulators and the S/dP tiles fit the register file.
+        for (int g = 0; g < PIPE - 1; ++g) ld(g);
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            if (g + PIPE - 1 < NG) ld(g + PIPE - 1);
+            s = mfma32(qa[g % PIPE], ka[g % PIPE], s);
+            dp = mfma32(oa[g % PIPE], va[g % PIPE], dp);
             __builtin_amdgcn_sched_barrier(0);
-            f32x16 s = mfma32(rd.a_operand(qt, 32 * sub, 0), k_operand(0), zero16());
-            f32x16 dp = mfma32(rd.a_operand(ot, 32 * sub, 0), v_operand(0), zero16());
+        }
 #pragma unroll
-            for (int g = 1; g < HD / 16; ++g) {
-                s = mfma32(rd.a_operand(qt, 32 * sub, g), k_operand(g), s);
-                dp = mfma32(rd.a_operand(ot, 32 * sub, g), v_operand(g), dp);
-            }
+        for (int r8 = 0; r8 < 2; ++r8) {
+            const int ql0 = r0 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
+            const f32x4 l_a = *reinterpret_cast<const f32x4 *>(lf + ql0);
+            const f32x4 l_b = *reinterpret_cast<const f32x4 *>(lf + ql0 + 4);
+            const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + BM + ql0);
+            const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + BM + ql0 + 4);
 #pragma unroll
-            for (int r8 = 0; r8 < 2; ++r8) {
-                const int ql0 = sub * 32 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
-                const f32x4 l_a = *reinterpret_cast<const f32x4 *>(lf + ql0);
-                const f32x4 l_b = *reinterpret_cast<const f32x4 *>(lf + ql0 + 4);
-                const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + BM + ql0);
-                const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + BM + ql0 + 4);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int r = 8 * r8 + u;
-                    const float l2 = u < 4 ? l_a[u] : l_b[u - 4];
-                    const float dsum = u < 4 ? d_a[u] : d_b[u - 4];
-                    float p = exp2_fast(fmaf(s[r], cs, -l2));
-                    if constexpr (MASK) {
-                        const int q = q0 + ql0 + u;
-                        const bool dead = q >= sq || !kv_ok || (CAUSAL && key > q + causal_off);
-                        p = dead ? 0.f : p;
-                    }
-                    s[r] = p;
-                    dp[r] = p * (dp[r] - dsum);
+            for (int u = 0; u < 8; ++u) {
+                const int r = 8 * r8 + u;
+                const float l2 = u < 4 ? l_a[u] : l_b[u - 4];
+                const float dsum = u < 4 ? d_a[u] : d_b[u - 4];
+                float p = exp2_fast(fmaf(s[r], cs, -l2));
+                if constexpr (MASK) {
+                    const int q = qh0 + 16 * r8 + 8 * hh + u;
+                    const bool dead = q >= sq || (CAUSAL && key > q + causal_off);
+                    p = dead ? 0.f : p;
                 }
+                s[r] = p;
+                dp[r] = p * (dp[r] - dsum);
             }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 pB[2], dsB[2];
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+            pB[gg] = pack8(s, 8 * gg);
+            dsB[gg] = pack8(dp, 8 * gg);
+        }
+        // Step t = (dt, gg): dV^T[dt] += dO^T P and dK^T[dt] += Q^T dS, the
+        // transposed operands read PIPE steps ahead.
+        constexpr int NT2 = 2 * (HD / 32);
+        f16x8 ta[PIPE], tq[PIPE];
+        auto ldt = [&](int t) {
+            ta[t % PIPE] = rd.tr_operand(ot, r0 + 16 * (t & 1), t >> 1);
+            tq[t % PIPE] = rd.tr_operand(qt, r0 + 16 * (t & 1), t >> 1);
+        };
+#pragma unroll
+        for (int t = 0; t < PIPE - 1; ++t) ldt(t);
+#pragma unroll
+        for (int t = 0; t < NT2; ++t) {
+            if (t + PIPE - 1 < NT2) ldt(t + PIPE - 1);
+            dv[t >> 1] = mfma32(ta[t % PIPE], pB[t & 1], dv[t >> 1]);
+            dk[t >> 1] = mfma32(tq[t % PIPE], dsB[t & 1], dk[t >> 1]);
             __builtin_amdgcn_sched_barrier(0);
-            f16x8 pB[2], dsB[2];
-#pragma unroll
-            for (int gg = 0; gg < 2; ++gg) {
-                pB[gg] = pack8(s, 8 * gg);
-                dsB[gg] = pack8(dp, 8 * gg);
-            }
-#pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-                for (int gg = 0; gg < 2; ++gg) {
-                    dv[dt] = mfma32(rd.tr_operand(ot, sub * 32 + 16 * gg, dt), pB[gg], dv[dt]);
-                    dk[dt] = mfma32(rd.tr_operand(qt, sub * 32 + 16 * gg, dt), dsB[gg], dk[dt]);
-                }
         }
     };
 
-    if (total > 0) issue(0, 0);
-    for (int j = 0; j < total; ++j) {
+    // Each wave walks the same sequence of blocks (one barrier per block) in
+    // four straight loops per q-head: blocks whose half sees none of its keys
+    // (skipped), diagonal blocks (masked), full blocks, and a ragged last
+    // block (masked).  Straight loops keep the dK/dV accumulators in place;
+    // branching per block would copy them at every join.  Keys past the
+    // sequence need no mask: their columns are never stored.
+    auto step = [&](int j, auto mask_tag, bool compute) {
         wait_vmem();
         __syncthreads();  // block j is in LDS; every wave is done with stage (j & 1) ^ 1
         if (j + 1 < total) issue(j + 1, (j & 1) ^ 1);
-        const int q0 = (m_first + j % n_qb) * BM;
-        if (CAUSAL && q0 + BM - 1 + causal_off < kw0) continue;  // no query of the block sees these keys
-        const bool need_mask = q0 + BM > sq || kw0 + 32 > sk || (CAUSAL && kw0 + 31 > q0 + causal_off);
-        if (need_mask)
-            block(j, q0, std::true_type{});
-        else
-            block(j, q0, std::false_type{});
+        if (compute) block(j, (m_first + j % n_qb) * BM + 32 * half, mask_tag);
+    };
+    auto clampi = [](int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); };
+    // Smallest block index i whose half start (m_first + i) * BM + 32 * half reaches x.
+    auto first_at = [&](int x) { return ((x - 32 * half + BM - 1) >> 6) - m_first; };
+    static_assert(BM == 64, "first_at divides by 64");
+    const int i1 = CAUSAL ? clampi(first_at(kw0 - 31 - causal_off), 0, n_qb) : 0;
+    const int i2 = CAUSAL ? clampi(first_at(kw0 + 31 - causal_off), i1, n_qb) : 0;
+    const int i3 = clampi(first_at(sq - 31), i2, n_qb);
+    if (total > 0) issue(0, 0);
+    for (int base = 0; base < total; base += n_qb) {
+        for (int i = 0; i < i1; ++i) step(base + i, std::true_type{}, false);
+        for (int i = i1; i < i2; ++i) step(base + i, std::true_type{}, true);
+        for (int i = i2; i < i3; ++i) step(base + i, std::false_type{}, true);
+        for (int i = i3; i < n_qb; ++i) step(base + i, std::true_type{}, true);
     }
 
-    if (kv_ok) {
-        f16 *krow = dkp + int64_t(key) * a.dk.row_stride;
-        f16 *vrow = dvp + int64_t(key) * a.dv.row_stride;
+    // Partial sums: half 1 hands over its dK, half 0 its dV (lane-contiguous
+    // fp32, conflict-free), then half 0 finishes dK and half 1 dV.
+    __syncthreads();  // every wave is done with the tiles
+    float *xk = reinterpret_cast<float *>(smem) + kg * (HD / 32) * 16 * 64;
+    float *xv = xk + 4 * (HD / 32) * 16 * 64;
+    if (half) {
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                f16x4 kv4, vv4;
+            for (int r = 0; r < 16; ++r) xk[(dt * 16 + r) * 64 + lane] = dk[dt][r];
+    } else {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    kv4[t] = (f16)(dk[dt][4 * a4 + t] * a.softmax_scale);
-                    vv4[t] = (f16)dv[dt][4 * a4 + t];
-                }
-                *reinterpret_cast<f16x4 *>(krow + dt * 32 + 8 * a4 + 4 * hh) = kv4;
-                *reinterpret_cast<f16x4 *>(vrow + dt * 32 + 8 * a4 + 4 * hh) = vv4;
-            }
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xv[(dt * 16 + r) * 64 + lane] = dv[dt][r];
     }
+    __syncthreads();
+    if (!kv_ok) return;
+    const fa_tensor &out_t = half ? a.dv : a.dk;
+    f16 *orow = (f16 *)out_t.ptr + base_off(out_t, packed_k, b, si.k_start, hk) + int64_t(key) * out_t.row_stride;
+    const float *xin = half ? xv : xk;
+    const float oscale = half ? 1.f : a.softmax_scale;
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+            f16x4 o4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int r = 4 * a4 + t;
+                const float mine = half ? dv[dt][r] : dk[dt][r];
+                o4[t] = (f16)((mine + xin[(dt * 16 + r) * 64 + lane]) * oscale);
+            }
+            *reinterpret_cast<f16x4 *>(orow + dt * 32 + 8 * a4 + 4 * hh) = o4;
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -491,7 +519,7 @@ static int launch_dkdv(const fa_bwd_args &a, hipStream_t s) {
     const int nnb = (a.seqlen_k + DkvCfg<HD>::BN - 1) / DkvCfg<HD>::BN;
     const int64_t grid = int64_t(nnb) * a.batch * a.nheads_k;
     if (grid == 0) return FA_OK;
-    hipLaunchKernelGGL((bwd_dkdv_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kDkvThreads), 0, s, a);
     return int(hipGetLastError());
 }
 
