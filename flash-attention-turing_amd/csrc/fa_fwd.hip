@@ -27,22 +27,38 @@ namespace fa {
 
 template <int HD>
 struct FwdCfg {
-    static constexpr int BM = 128;                // queries per workgroup
-    static constexpr int BN = 64;                 // keys per block
     static constexpr int NT = 256;                // threads
+    static constexpr int OCC = 2;                 // workgroups per CU
+    static constexpr int BM = 32 * (NT / 64);     // queries per workgroup (32 per wave)
+    static constexpr int BN = 64;                 // keys per block
     static constexpr int KCH = HD / 8;            // 16-byte chunks per row
     static constexpr int TILE = BN * HD * 2;      // one K or V tile
     static constexpr int STAGE = 2 * TILE;        // K tile, then V tile
 };
 
-// The running maximum a row's probabilities are taken against is raised (and
-// O, l rescaled) only in the blocks where some row of the wave finds a larger
-// score; the wave skips the rescale otherwise.  The maximum is never left
-// stale: with P = exp2(S*c - m) the row's largest probability is exactly 1,
-// which keeps the fp16 rounding of P (and so O's error) at the reference's
-// level for sharply peaked rows.
+// The running maximum m a row's probabilities P = exp2(S*c - m) are taken
+// against is raised (and O, l rescaled) only in the blocks where some row of
+// the wave finds a score more than kRescaleSlack above it, so most blocks skip
+// the rescale; P then stays below 2^kRescaleSlack, well inside fp16.  O is
+// normalised by the sum of the fp16-rounded P that the PV product used
+// (l_o), so O = sum P V / l_o is built from consistent weights: a row
+// dominated by one key returns that key's V exactly whatever the stale
+// maximum, as it does with P = 1 in the reference.  The LSE uses the fp32 sum
+// of the unrounded P (l_p), as the reference does.
+constexpr float kRescaleSlack = 8.f;
+
+// Sum of the eight fp16 values of an MFMA operand, accumulated in fp32.
+__device__ __forceinline__ float sum8(const f16x8 &v, float acc) {
+    typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {f16(1), f16(1)};
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
+}
+
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
+__global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
     using C = FwdCfg<HD>;
     constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
@@ -102,7 +118,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
     float m_t = -INFINITY;  // reference max of scale*log2(e)*S for this lane's query
-    float l_p = 0.f;        // partial row sum over this lane half's keys
+    float l_p = 0.f;        // partial row sum over this lane half's keys (fp32 P, for the LSE)
+    float l_o = 0.f;        // the same over the fp16-rounded P (normalises O)
 
     TileReader<HD> rd;
     rd.init(lane);
@@ -159,10 +176,11 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
-        if (__builtin_amdgcn_ballot_w64(mx_t > m_t) != 0) {
+        if (__builtin_amdgcn_ballot_w64(mx_t > m_t + kRescaleSlack) != 0) {
             const float m_new = fmaxf(m_t, mx_t);
             const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
             l_p *= alpha;
+            l_o *= alpha;
 #pragma unroll
             for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
@@ -182,10 +200,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
                 rs += p;
             }
         l_p += rs;
-
         f16x8 pB[4];
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+        for (int gg = 0; gg < 4; ++gg) {
+            pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+            l_o = sum8(pB[gg], l_o);
+        }
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
@@ -202,8 +222,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
 
     // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
     const float l_tot = l_p + __shfl_xor(l_p, 32);
+    const float lo_tot = l_o + __shfl_xor(l_o, 32);
     if (qi < sq) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        const float inv = lo_tot > 0.f ? 1.f / lo_tot : 0.f;
         f16 *orow = op + int64_t(qi) * ors;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
