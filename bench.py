@@ -179,7 +179,7 @@ def decode_setup(device, seed=3):
     lse = torch.empty((b, h, 1), dtype=torch.float32, device=device)
     rows = b * h
     ws = torch.empty(splits * rows * (d + 1), dtype=torch.float32, device=device)
-    order = torch.empty(b, dtype=torch.int32, device=device)
+    order = torch.empty(b + 1, dtype=torch.int32, device=device)  # ranks + work counter
     args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, seqlens, d ** -0.5, True, splits, k_new=k_new,
                                 v_new=v_new, block_table=table_d, out_accum=ws[: splits * rows * d],
                                 lse_accum=ws[splits * rows * d :], batch_order=order)
@@ -254,7 +254,7 @@ def longctx_setup(device, seed=4):
     lse = torch.empty((b, h, sq), dtype=torch.float32, device=device)
     nrow = b * h * sq
     ws = torch.empty(splits * nrow * (d + 1), dtype=torch.float32, device=device)
-    order = torch.empty(b, dtype=torch.int32, device=device)
+    order = torch.empty(b + 1, dtype=torch.int32, device=device)  # ranks + work counter
     args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, lens.to(torch.int32).to(device), d ** -0.5, True,
                                 splits, k_new=k_new, v_new=v_new, cache_batch_idx=batch_idx.to(device),
                                 out_accum=ws[: splits * nrow * d], lse_accum=ws[splits * nrow * d :],

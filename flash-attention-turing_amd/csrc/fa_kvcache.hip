@@ -25,11 +25,12 @@
 // keeps its own online softmax state; the four waves merge their partial
 // states through LDS at the end.  Paged, remapped and contiguous caches take
 // the same tile order and the same arithmetic, so their results are
-// bit-identical for the same logical cache.  The grid is 1-D with the
+// bit-identical for the same logical cache.  Work items are ordered with the
 // sequence rank slowest: when the caller passes a batch_order workspace, a
-// one-workgroup kernel first ranks the sequences by key count (longest
-// first), so the longest sequences start first and the short ones fill the
-// tail of the launch.
+// one-workgroup kernel first ranks the sequences by key count (longest first)
+// and a resident grid of two workgroups per CU deals the items out from a
+// device counter in that order, so the longest sequences start first, the
+// short ones fill the end, and no workgroup is relaunched between items.
 #include <algorithm>
 #include <type_traits>
 
@@ -98,243 +99,258 @@ struct KvCfg {
     static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
 };
 
-template <int HD>
+// Work items are (sequence rank, split, kv head, row tile), rank slowest: with
+// batch_order the longest sequences' items come first (longest-job-first keeps
+// the last items short).  With DYN the grid is resident (two workgroups per
+// CU) and each workgroup, after its first item blockIdx.x, takes the next
+// unclaimed item from a device counter, so no workgroup is relaunched and
+// the items are dealt out greedily in that order.  The counter
+// (batch_order[batch]) is zeroed by kv_order_kernel on the same stream.
+template <int HD, bool DYN>
 __global__ __launch_bounds__(256, KvCfg<HD>::NST == 1 ? 2 : 1) void kv_splitkv_kernel(const fa_kvcache_args a,
-                                                                                   const int row_tiles) {
+                                                                                   const int row_tiles,
+                                                                                   const int n_items) {
     using C = KvCfg<HD>;
     __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
     __shared__ int pages[C::MAX_PAGES];
+    __shared__ int next_item;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int col = lane & 31, hh = lane >> 5;
-    // One-dimensional grid, sequence rank slowest: with batch_order the
-    // longest sequences' workgroups are dispatched first (longest-job-first
-    // keeps the last wave of workgroups short).
-    int rest = blockIdx.x;
-    const int rt = rest % row_tiles;
-    rest /= row_tiles;
-    const int hk = rest % a.nheads_k;
-    rest /= a.nheads_k;
-    const int split = rest % a.num_splits;
-    const int rank = rest / a.num_splits;
-    const int b = a.batch_order ? a.batch_order[rank] : rank;
-    const int G = a.nheads / a.nheads_k;
-    const int R = G * a.seqlen_q;  // rows of this (batch, kv head): row = qpos * G + g
+    for (int item = blockIdx.x; item < n_items;) {
+        int rest = item;
+        const int rt = rest % row_tiles;
+        rest /= row_tiles;
+        const int hk = rest % a.nheads_k;
+        rest /= a.nheads_k;
+        const int split = rest % a.num_splits;
+        const int rank = rest / a.num_splits;
+        const int b = a.batch_order ? a.batch_order[rank] : rank;
+        const int G = a.nheads / a.nheads_k;
+        const int R = G * a.seqlen_q;  // rows of this (batch, kv head): row = qpos * G + g
 
-    const int L = a.cache_seqlens[b] + a.seqlen_new;
-    const int S = a.num_splits;
-    const int s0 = int((int64_t(L) * split) / S), s1 = int((int64_t(L) * (split + 1)) / S);
-    const int cache_row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
+        const int L = a.cache_seqlens[b] + a.seqlen_new;
+        const int S = a.num_splits;
+        const int s0 = int((int64_t(L) * split) / S), s1 = int((int64_t(L) * (split + 1)) / S);
+        const int cache_row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
 
-    // This lane's query row.
-    const int row = rt * 32 + col;
-    const bool row_ok = row < R;
-    const int qpos = row_ok ? row / G : 0;
-    const int hq = hk * G + (row_ok ? row % G : 0);
-    const int lim = a.causal ? qpos + L - a.seqlen_q : L - 1;  // last visible key
+        // This lane's query row.
+        const int row = rt * 32 + col;
+        const bool row_ok = row < R;
+        const int qpos = row_ok ? row / G : 0;
+        const int hq = hk * G + (row_ok ? row % G : 0);
+        const int lim = a.causal ? qpos + L - a.seqlen_q : L - 1;  // last visible key
 
-    const bool neg = a.softmax_scale < 0.f;
-    const float cscale = fabsf(a.softmax_scale) * kLog2e;
-    f16x8 qB[HD / 16];
-    {
-        const f16 *qp = (const f16 *)a.q.ptr + int64_t(b) * a.q.batch_stride + int64_t(qpos) * a.q.row_stride +
-                        int64_t(hq) * a.q.head_stride;
-#pragma unroll
-        for (int g = 0; g < HD / 16; ++g) {
-            u32x4 v = row_ok ? ldg16(qp + 16 * g + 8 * hh) : zero_u4();
-            if (neg) v = neg_h8(v);
-            qB[g] = as_h8(v);
+        const bool neg = a.softmax_scale < 0.f;
+        const float cscale = fabsf(a.softmax_scale) * kLog2e;
+        f16x8 qB[HD / 16];
+        {
+            const f16 *qp = (const f16 *)a.q.ptr + int64_t(b) * a.q.batch_stride + int64_t(qpos) * a.q.row_stride +
+                            int64_t(hq) * a.q.head_stride;
+    #pragma unroll
+            for (int g = 0; g < HD / 16; ++g) {
+                u32x4 v = row_ok ? ldg16(qp + 16 * g + 8 * hh) : zero_u4();
+                if (neg) v = neg_h8(v);
+                qB[g] = as_h8(v);
+            }
         }
-    }
 
-    f32x16 o[HD / 32];
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
-    float m_t = -INFINITY, l_p = 0.f;
+        f32x16 o[HD / 32];
+    #pragma unroll
+        for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
+        float m_t = -INFINITY, l_p = 0.f;
 
-    const int t_first = s0 / kTile;
-    const int t_last = s1 > s0 ? (s1 - 1) / kTile : t_first - 1;
-    const int my_first = t_first + wave;
-    const int n_my = my_first <= t_last ? (t_last - my_first) / kKvWaves + 1 : 0;
+        const int t_first = s0 / kTile;
+        const int t_last = s1 > s0 ? (s1 - 1) / kTile : t_first - 1;
+        const int my_first = t_first + wave;
+        const int n_my = my_first <= t_last ? (t_last - my_first) / kKvWaves + 1 : 0;
 
-    // Page ids of the split, staged in LDS so the ring never waits on a table read.
-    const int page = a.page_block_size;
-    const int pg_first = a.block_table ? (t_first * kTile) / page : 0;
-    const int n_pages = a.block_table && s1 > s0 ? (t_last * kTile) / page - pg_first + 1 : 0;
-    const bool pages_in_lds = n_pages <= C::MAX_PAGES;
-    if (a.block_table && pages_in_lds) {
-        const int32_t *bt = a.block_table + int64_t(b) * a.block_table_stride + pg_first;
-        for (int i = tid; i < n_pages; i += kKvThreads) pages[i] = bt[i];
-    }
-    __syncthreads();
+        // Page ids of the split, staged in LDS so the ring never waits on a table read.
+        const int page = a.page_block_size;
+        const int pg_first = a.block_table ? (t_first * kTile) / page : 0;
+        const int n_pages = a.block_table && s1 > s0 ? (t_last * kTile) / page - pg_first + 1 : 0;
+        const bool pages_in_lds = n_pages <= C::MAX_PAGES;
+        if (a.block_table && pages_in_lds) {
+            const int32_t *bt = a.block_table + int64_t(b) * a.block_table_stride + pg_first;
+            for (int i = tid; i < n_pages; i += kKvThreads) pages[i] = bt[i];
+        }
+        __syncthreads();
 
-    const int64_t krs = a.k_cache.row_stride, vrs = a.v_cache.row_stride;
+        const int64_t krs = a.k_cache.row_stride, vrs = a.v_cache.row_stride;
 
-    // The tile loop, instantiated twice: with the split's page ids in LDS (and
-    // no other vector-memory load while copies are in flight), and a fallback
-    // that reads the block table per tile for splits spanning more pages.
-    auto run = [&](auto lds_pages_tag) {
-    constexpr bool LDS_PAGES = decltype(lds_pages_tag)::value;
-    // Copy tile t into ring stage st of this wave.  Rows past L re-read key L - 1
-    // of the same tile (finite values; masked below).
-    auto issue = [&](int t, int st) {
-        const int p0 = t * kTile;
-        int64_t koff, voff;
-        if (a.block_table) {
-            const int pi = p0 / page;
-            int blk;
-            if constexpr (LDS_PAGES)
-                blk = pages[pi - pg_first];
+        // The tile loop, instantiated twice: with the split's page ids in LDS (and
+        // no other vector-memory load while copies are in flight), and a fallback
+        // that reads the block table per tile for splits spanning more pages.
+        auto run = [&](auto lds_pages_tag) {
+        constexpr bool LDS_PAGES = decltype(lds_pages_tag)::value;
+        // Copy tile t into ring stage st of this wave.  Rows past L re-read key L - 1
+        // of the same tile (finite values; masked below).
+        auto issue = [&](int t, int st) {
+            const int p0 = t * kTile;
+            int64_t koff, voff;
+            if (a.block_table) {
+                const int pi = p0 / page;
+                int blk;
+                if constexpr (LDS_PAGES)
+                    blk = pages[pi - pg_first];
+                else
+                    blk = a.block_table[int64_t(b) * a.block_table_stride + pi];
+                const int in_page = p0 - pi * page;
+                koff = int64_t(blk) * a.k_cache.batch_stride + int64_t(in_page) * krs;
+                voff = int64_t(blk) * a.v_cache.batch_stride + int64_t(in_page) * vrs;
+            } else {
+                koff = int64_t(cache_row) * a.k_cache.batch_stride + int64_t(p0) * krs;
+                voff = int64_t(cache_row) * a.v_cache.batch_stride + int64_t(p0) * vrs;
+            }
+            const f16 *kb = (const f16 *)a.k_cache.ptr + koff + int64_t(hk) * a.k_cache.head_stride;
+            const f16 *vb = (const f16 *)a.v_cache.ptr + voff + int64_t(hk) * a.v_cache.head_stride;
+            char *ks = smem + (wave * C::NST + st) * C::STAGE;
+            char *vs = ks + C::TILE;
+            dma_tile<HD, kTile, 64>(ks, kb, krs, 0, L - 1 - p0, 0, lane);
+            dma_tile<HD, kTile, 64>(vs, vb, vrs, 0, L - 1 - p0, 0, lane);
+        };
+
+        TileReader<HD> rd;
+        rd.init(lane);
+        if (n_my > 0) issue(my_first, 0);
+        if (C::NST > 1 && n_my > 1) issue(my_first + kKvWaves, 1);
+        for (int k = 0; k < n_my; ++k) {
+            const int st = k % C::NST;
+            if (k + 1 < n_my)
+                wait_vmem_n<(C::NST - 1) * 2 * C::CPW>();  // newer tiles may stay in flight
             else
-                blk = a.block_table[int64_t(b) * a.block_table_stride + pi];
-            const int in_page = p0 - pi * page;
-            koff = int64_t(blk) * a.k_cache.batch_stride + int64_t(in_page) * krs;
-            voff = int64_t(blk) * a.v_cache.batch_stride + int64_t(in_page) * vrs;
-        } else {
-            koff = int64_t(cache_row) * a.k_cache.batch_stride + int64_t(p0) * krs;
-            voff = int64_t(cache_row) * a.v_cache.batch_stride + int64_t(p0) * vrs;
+                wait_vmem();
+            const char *ks = smem + (wave * C::NST + st) * C::STAGE;
+            const char *vs = ks + C::TILE;
+            const int p0 = (my_first + k * kKvWaves) * kTile;
+            // All operands of the tile into registers first, then refill the stage
+            // right away: two tiles stay in flight while this one is computed.
+            f16x8 ka[HD / 16], va[HD / 32][2];
+    #pragma unroll
+            for (int g = 0; g < HD / 16; ++g) ka[g] = rd.a_operand(ks, 0, g);
+    #pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt)
+    #pragma unroll
+                for (int gg = 0; gg < 2; ++gg) va[dt][gg] = rd.tr_operand(vs, 16 * gg, dt);
+            wait_lds();
+            if (k + C::NST < n_my) issue(my_first + (k + C::NST) * kKvWaves, st);
+            f32x16 s = mfma32(ka[0], qB[0], zero16());
+    #pragma unroll
+            for (int g = 1; g < HD / 16; ++g) s = mfma32(ka[g], qB[g], s);
+            float mx = -INFINITY;
+    #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = p0 + acc_lrow(r, hh);
+                if (key < s0 || key >= s1 || key > lim) s[r] = -INFINITY;
+                mx = fmaxf(mx, s[r]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
+            const float m_new = fmaxf(m_t, mx_t);
+            const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            float rs = 0.f;
+    #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = s[r] == -INFINITY ? 0.f : exp2_fast(fmaf(s[r], cscale, -m_use));
+                s[r] = p;
+                rs += p;
+            }
+            l_p = l_p * alpha + rs;
+            m_t = m_new;
+            // P stays fp32-accurate through the product: P = hi + lo with both halves fp16.
+            f16x8 ph[2], pl[2];
+    #pragma unroll
+            for (int gg = 0; gg < 2; ++gg)
+    #pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const float p = s[8 * gg + u];
+                    const f16 hi = (f16)p;
+                    ph[gg][u] = hi;
+                    pl[gg][u] = (f16)(p - float(hi));
+                }
+    #pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt) {
+    #pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    #pragma unroll
+                for (int gg = 0; gg < 2; ++gg) {
+                    o[dt] = mfma32(va[dt][gg], ph[gg], o[dt]);
+                    o[dt] = mfma32(va[dt][gg], pl[gg], o[dt]);
+                }
+            }
         }
-        const f16 *kb = (const f16 *)a.k_cache.ptr + koff + int64_t(hk) * a.k_cache.head_stride;
-        const f16 *vb = (const f16 *)a.v_cache.ptr + voff + int64_t(hk) * a.v_cache.head_stride;
-        char *ks = smem + (wave * C::NST + st) * C::STAGE;
-        char *vs = ks + C::TILE;
-        dma_tile<HD, kTile, 64>(ks, kb, krs, 0, L - 1 - p0, 0, lane);
-        dma_tile<HD, kTile, 64>(vs, vb, vrs, 0, L - 1 - p0, 0, lane);
-    };
-
-    TileReader<HD> rd;
-    rd.init(lane);
-    if (n_my > 0) issue(my_first, 0);
-    if (C::NST > 1 && n_my > 1) issue(my_first + kKvWaves, 1);
-    for (int k = 0; k < n_my; ++k) {
-        const int st = k % C::NST;
-        if (k + 1 < n_my)
-            wait_vmem_n<(C::NST - 1) * 2 * C::CPW>();  // newer tiles may stay in flight
+        };
+        if (pages_in_lds)
+            run(std::true_type{});
         else
-            wait_vmem();
-        const char *ks = smem + (wave * C::NST + st) * C::STAGE;
-        const char *vs = ks + C::TILE;
-        const int p0 = (my_first + k * kKvWaves) * kTile;
-        // All operands of the tile into registers first, then refill the stage
-        // right away: two tiles stay in flight while this one is computed.
-        f16x8 ka[HD / 16], va[HD / 32][2];
-#pragma unroll
-        for (int g = 0; g < HD / 16; ++g) ka[g] = rd.a_operand(ks, 0, g);
-#pragma unroll
+            run(std::false_type{});
+
+        // Merge the four waves: each publishes (m, l) per row and its O^T tile.
+        const float l_w = l_p + __shfl_xor(l_p, 32);
+        float *mrow = reinterpret_cast<float *>(smem + kKvWaves * C::WAVE_LDS);
+        float *lrow = mrow + kKvWaves * 32;
+        __syncthreads();  // every wave is done with its ring
+        float *ow = reinterpret_cast<float *>(smem + wave * C::WAVE_LDS);  // [HD][32] fp32
+    #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-            for (int gg = 0; gg < 2; ++gg) va[dt][gg] = rd.tr_operand(vs, 16 * gg, dt);
-        wait_lds();
-        if (k + C::NST < n_my) issue(my_first + (k + C::NST) * kKvWaves, st);
-        f32x16 s = mfma32(ka[0], qB[0], zero16());
-#pragma unroll
-        for (int g = 1; g < HD / 16; ++g) s = mfma32(ka[g], qB[g], s);
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = p0 + acc_lrow(r, hh);
-            if (key < s0 || key >= s1 || key > lim) s[r] = -INFINITY;
-            mx = fmaxf(mx, s[r]);
+    #pragma unroll
+            for (int r = 0; r < 16; ++r) ow[(dt * 32 + acc_row(r, hh)) * 32 + col] = o[dt][r];
+        if (hh == 0) {
+            mrow[wave * 32 + col] = m_t;
+            lrow[wave * 32 + col] = l_w;
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
-        const float m_new = fmaxf(m_t, mx_t);
-        const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        float rs = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p = s[r] == -INFINITY ? 0.f : exp2_fast(fmaf(s[r], cscale, -m_use));
-            s[r] = p;
-            rs += p;
-        }
-        l_p = l_p * alpha + rs;
-        m_t = m_new;
-        // P stays fp32-accurate through the product: P = hi + lo with both halves fp16.
-        f16x8 ph[2], pl[2];
-#pragma unroll
-        for (int gg = 0; gg < 2; ++gg)
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float p = s[8 * gg + u];
-                const f16 hi = (f16)p;
-                ph[gg][u] = hi;
-                pl[gg][u] = (f16)(p - float(hi));
-            }
-#pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-#pragma unroll
-            for (int gg = 0; gg < 2; ++gg) {
-                o[dt] = mfma32(va[dt][gg], ph[gg], o[dt]);
-                o[dt] = mfma32(va[dt][gg], pl[gg], o[dt]);
-            }
-        }
-    }
-    };
-    if (pages_in_lds)
-        run(std::true_type{});
-    else
-        run(std::false_type{});
+        __syncthreads();
 
-    // Merge the four waves: each publishes (m, l) per row and its O^T tile.
-    const float l_w = l_p + __shfl_xor(l_p, 32);
-    float *mrow = reinterpret_cast<float *>(smem + kKvWaves * C::WAVE_LDS);
-    float *lrow = mrow + kKvWaves * 32;
-    __syncthreads();  // every wave is done with its ring
-    float *ow = reinterpret_cast<float *>(smem + wave * C::WAVE_LDS);  // [HD][32] fp32
-#pragma unroll
-    for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ow[(dt * 32 + acc_row(r, hh)) * 32 + col] = o[dt][r];
-    if (hh == 0) {
-        mrow[wave * 32 + col] = m_t;
-        lrow[wave * 32 + col] = l_w;
-    }
-    __syncthreads();
-
-    const int rows_here = min(32, R - rt * 32);
-    const int nrow_all = a.batch * a.nheads * a.seqlen_q;
-    for (int e = tid; e < rows_here * HD; e += kKvThreads) {
-        const int c = e / HD, d = e % HD;
-        float mstar = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kKvWaves; ++w) mstar = fmaxf(mstar, mrow[w * 32 + c]);
-        float lsum = 0.f, acc = 0.f;
-        if (mstar != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < kKvWaves; ++w) {
-                const float mw = mrow[w * 32 + c];
-                const float sc = mw == -INFINITY ? 0.f : exp2_fast(mw - mstar);
-                lsum += lrow[w * 32 + c] * sc;
-                acc += reinterpret_cast<const float *>(smem + w * C::WAVE_LDS)[d * 32 + c] * sc;
+        const int rows_here = min(32, R - rt * 32);
+        const int nrow_all = a.batch * a.nheads * a.seqlen_q;
+        for (int e = tid; e < rows_here * HD; e += kKvThreads) {
+            const int c = e / HD, d = e % HD;
+            float mstar = -INFINITY;
+    #pragma unroll
+            for (int w = 0; w < kKvWaves; ++w) mstar = fmaxf(mstar, mrow[w * 32 + c]);
+            float lsum = 0.f, acc = 0.f;
+            if (mstar != -INFINITY) {
+    #pragma unroll
+                for (int w = 0; w < kKvWaves; ++w) {
+                    const float mw = mrow[w * 32 + c];
+                    const float sc = mw == -INFINITY ? 0.f : exp2_fast(mw - mstar);
+                    lsum += lrow[w * 32 + c] * sc;
+                    acc += reinterpret_cast<const float *>(smem + w * C::WAVE_LDS)[d * 32 + c] * sc;
+                }
+            }
+            const bool live = lsum > 0.f;
+            const float outv = live ? acc / lsum : 0.f;
+            const float lse = live ? (mstar + log2_fast(lsum)) * kLn2 : -INFINITY;
+            const int r = rt * 32 + c;
+            const int qp = r / G, h = hk * G + r % G;
+            const int64_t orow = (int64_t(b) * a.nheads + h) * a.seqlen_q + qp;  // (batch, head, qpos)
+            if (S == 1) {
+                f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
+                          int64_t(h) * a.o.head_stride;
+                op[d] = (f16)outv;
+                if (d == 0) a.lse[orow] = live ? lse : 0.f;
+            } else {
+                a.out_accum[(int64_t(split) * nrow_all + orow) * HD + d] = outv;
+                if (d == 0) a.lse_accum[int64_t(split) * nrow_all + orow] = lse;
             }
         }
-        const bool live = lsum > 0.f;
-        const float outv = live ? acc / lsum : 0.f;
-        const float lse = live ? (mstar + log2_fast(lsum)) * kLn2 : -INFINITY;
-        const int r = rt * 32 + c;
-        const int qp = r / G, h = hk * G + r % G;
-        const int64_t orow = (int64_t(b) * a.nheads + h) * a.seqlen_q + qp;  // (batch, head, qpos)
-        if (S == 1) {
-            f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
-                      int64_t(h) * a.o.head_stride;
-            op[d] = (f16)outv;
-            if (d == 0) a.lse[orow] = live ? lse : 0.f;
-        } else {
-            a.out_accum[(int64_t(split) * nrow_all + orow) * HD + d] = outv;
-            if (d == 0) a.lse_accum[int64_t(split) * nrow_all + orow] = lse;
-        }
+        if constexpr (!DYN) break;
+        __syncthreads();  // every thread is done with this item's LDS
+        if (tid == 0) next_item = atomicAdd(a.batch_order + a.batch, 1) + int(gridDim.x);
+        __syncthreads();
+        item = next_item;
     }
 }
 
 // ---------------------------------------------------------------------------
 // batch_order[r] = the sequence with the r-th largest key count (ties by index).
 constexpr int kOrderMaxBatch = 2048;
+// It also zeroes the work counter batch_order[batch] of the resident split kernel.
 __global__ __launch_bounds__(256) void kv_order_kernel(const fa_kvcache_args a) {
     __shared__ int lens[kOrderMaxBatch];
+    if (threadIdx.x == 0) a.batch_order[a.batch] = 0;
     for (int i = threadIdx.x; i < a.batch; i += 256) lens[i] = a.cache_seqlens[i];
     __syncthreads();
     for (int i = threadIdx.x; i < a.batch; i += 256) {
@@ -374,6 +390,19 @@ __global__ __launch_bounds__(256) void kv_combine_kernel(const fa_kvcache_args a
         op[d] = (f16)acc;
     }
     if (lane == 0) a.lse[r] = live ? ltot : 0.f;
+}
+
+// Compute units of the current device, queried once per device.
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
 }
 
 static int check_kv(const fa_kvcache_args *p) {
@@ -446,17 +475,31 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     if (gx > 0x7fffffff) return FA_ERR_INVALID_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     fa_kvcache_args run = a;
-    if (a.batch_order && a.batch > 1 && a.batch <= fa::kOrderMaxBatch) {
+    const int n_items = int(gx);
+    // With the batch_order workspace: rank the sequences and reset the work
+    // counter, then run a resident grid of two workgroups per CU that deals
+    // the items out in that order.  Without it: one workgroup per item.
+    const bool dyn = a.batch_order && a.batch <= fa::kOrderMaxBatch;
+    unsigned grid = unsigned(gx);
+    if (dyn) {
         hipLaunchKernelGGL(fa::kv_order_kernel, dim3(1), dim3(256), 0, s, a);
         const int rc = int(hipGetLastError());
         if (rc) return rc;
+        grid = unsigned(std::min<int64_t>(gx, 2 * int64_t(fa::device_cus())));
     } else {
         run.batch_order = nullptr;  // natural order
     }
-    if (a.head_dim == 128)
-        hipLaunchKernelGGL(fa::kv_splitkv_kernel<128>, dim3(unsigned(gx)), dim3(fa::kKvThreads), 0, s, run, row_tiles);
-    else
-        hipLaunchKernelGGL(fa::kv_splitkv_kernel<64>, dim3(unsigned(gx)), dim3(fa::kKvThreads), 0, s, run, row_tiles);
+    if (a.head_dim == 128) {
+        if (dyn)
+            hipLaunchKernelGGL((fa::kv_splitkv_kernel<128, true>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
+        else
+            hipLaunchKernelGGL((fa::kv_splitkv_kernel<128, false>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
+    } else {
+        if (dyn)
+            hipLaunchKernelGGL((fa::kv_splitkv_kernel<64, true>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
+        else
+            hipLaunchKernelGGL((fa::kv_splitkv_kernel<64, false>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
+    }
     return int(hipGetLastError());
 }
 

@@ -442,10 +442,10 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
                                         int(batch_size), int(num_heads), int(num_heads_k),
                                         num_cus(q.get_device()));
         // Workspace: split accumulators (num_splits > 1), then the longest-first
-        // sequence order the split kernel schedules by.
+        // sequence order the split kernel schedules by and its work counter.
         const int64_t rows = batch_size * num_heads * seqlen_q;
         const int64_t acc_floats = a.num_splits > 1 ? a.num_splits * rows * (head_size + 1) : 0;
-        at::Tensor ws = at::empty({acc_floats + batch_size}, q.options().dtype(at::kFloat));
+        at::Tensor ws = at::empty({acc_floats + batch_size + 1}, q.options().dtype(at::kFloat));
         if (a.num_splits > 1) {
             a.out_accum = ws.data_ptr<float>();
             a.lse_accum = a.out_accum + a.num_splits * rows * head_size;

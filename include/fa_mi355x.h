@@ -120,8 +120,9 @@ typedef struct fa_kvcache_args {
     int32_t causal;
     float *out_accum;               /* workspace [num_splits][batch*nheads*seqlen_q][d] fp32 */
     float *lse_accum;               /* workspace [num_splits][batch*nheads*seqlen_q] fp32    */
-    int32_t *batch_order;           /* workspace [batch]: sequences longest first (filled by
-                                       fa_kv_splitkv), or NULL for the natural order           */
+    int32_t *batch_order;           /* workspace [batch + 1]: sequences longest first and a work
+                                       counter (both filled by fa_kv_splitkv), or NULL for the
+                                       natural order                                           */
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);
@@ -129,7 +130,7 @@ typedef struct fa_kvcache_args {
 int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seqlen_q,
                      int batch, int nheads, int nheads_k, int num_cus);
 /* Bytes of the split accumulators for args->num_splits (0 when num_splits == 1);
- * batch_order, when used, needs batch * 4 more. */
+ * batch_order, when used, needs (batch + 1) * 4 more. */
 size_t fa_kv_workspace_bytes(const fa_kvcache_args *args);
 /* In-place append of k_new/v_new at cache_seqlens (contiguous, remapped or paged). */
 int fa_kv_append(const fa_kvcache_args *args, void *stream);
