@@ -46,10 +46,10 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 # (FETCH x 2.0, WRITE x 1.0); summary in profiles/hbm_bytes_pmc_c2_c4.md.
 # Re-measured whenever a kernel changes; None where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 6.801e8 + 6.816e7,
-    "bwd_dq": 6.148e8 + 7.350e7,
-    "bwd_dkdv": 7.397e8 + 1.645e8,
-    "kv_splitkv": 4.693e9 + 8.52e6,
+    "fwd": 8.102e8 + 6.816e7,
+    "bwd_dq": 6.205e8 + 7.345e7,
+    "bwd_dkdv": 7.514e8 + 1.452e8,
+    "kv_splitkv": 4.696e9 + 8.657e6,
 }
 
 
