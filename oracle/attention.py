@@ -195,6 +195,7 @@ def bwd_fp32_noise(
     softmax_scale: float,
     causal: bool,
     growth: float = 4.0,
+    dt: torch.dtype = torch.float64,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Per-element fp32 rounding-noise scale of (dq, dk, dv), in float32.
 
@@ -208,10 +209,11 @@ def bwd_fp32_noise(
         through absolute values, plus eps times the sum of |terms|;
     times ``growth`` for accumulation-order effects.  Where dP == D in real
     arithmetic (a row with one visible key, O = v) dS is pure noise of this
-    size, which the twin's fp16 rounding points cannot show.
+    size, which the twin's fp16 rounding points cannot show.  ``dt`` is the
+    evaluation type (every term is a sum of non-negative products, so float32
+    is enough for the full-size tests; float64 by default).
     """
     eps = torch.finfo(torch.float32).eps
-    dt = torch.float64
     b, sq, h, d = q.shape
     sk, hk = k.shape[1], k.shape[2]
     groups = h // hk

@@ -152,3 +152,30 @@ def test_kvcache_empty_cache_and_int_seqlens(device):
     out_full = fai.flash_attn_with_kvcache(q, kc, vc)  # cache_seqlens None -> full capacity
     o_ref, _ = okv.splitkv_attention(q.cpu(), kc.cpu(), vc.cpu(), torch.full((2,), 256), 0.125, False, 1)
     assert_2x("out", out_full, o_ref, o_ref.to(torch.float16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("page,hd,splits,scale", [(512, 128, 4, None), (768, 64, 0, -0.2), (1024, 128, 7, 0.05)])
+def test_kvcache_page_sizes_and_scales(device, page, hd, splits, scale):
+    """Pages larger than 256 tokens (any multiple of 256 is accepted), negative and
+    non-default scales: append bit-exact, attention vs the oracle, and, where the
+    contiguous cache takes the same split-KV kernel (explicit splits > 1; a
+    contiguous multi-token chunk otherwise runs the tiled forward kernel, as in
+    the reference's routing, flash_api.cpp:668), the same output bit for bit."""
+    g = torch.Generator().manual_seed(6000 + page + hd)
+    b, sq, h, hk, cap, new = 3, 2, 8, 2, 3 * page, 2
+    kc = randn16((b, cap, hk, hd), g)
+    vc = randn16((b, cap, hk, hd), g)
+    q = randn16((b, sq, h, hd), g)
+    k = randn16((b, new, hk, hd), g)
+    v = randn16((b, new, hk, hd), g)
+    seqlens = torch.tensor([cap - new, page - 1, 5], dtype=torch.int32)  # full, straddling a page end, short
+    kp, vp, table = _paged_from_contiguous(kc, vc, seqlens, page, g)
+    out, lse, kp_after, vp_after = _run(device, q, kp, vp, k, v, seqlens, None, table, True, splits, scale)
+    o_ref, l_ref, kp_ref, vp_ref = _oracle(q, kp, vp, k, v, seqlens, None, table, True, splits, scale)
+    assert torch.equal(kp_after, kp_ref) and torch.equal(vp_after, vp_ref)
+    assert_2x("out", out, o_ref, o_ref.to(torch.float16))
+    assert_lse(lse, l_ref)
+    if splits > 1:
+        contiguous = _run(device, q, kc, vc, k, v, seqlens, None, None, True, splits, scale)
+        assert torch.equal(contiguous[0], out) and torch.equal(contiguous[1], lse)
