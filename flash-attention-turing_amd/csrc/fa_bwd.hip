@@ -144,8 +144,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         char *ks = smem + st * C::STAGE;
         const int n0 = nb * BN;
         if (n0 + BN <= sk) {
-            kcp.copy(ks, kp + int64_t(n0) * krs, krs);
-            vcp.copy(ks + C::TILE, vp + int64_t(n0) * vrs, vrs);
+            kcp.copy_to(lds_addr(smem) + st * C::STAGE, kp + int64_t(n0) * krs, krs);
+            vcp.copy_to(lds_addr(smem) + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
         } else {
             dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
             dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
@@ -302,33 +302,39 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     // Query blocks that can see this key block, repeated for each q-head of the group.
     const int m_first = CAUSAL ? max(0, k0 - causal_off) / BM : 0;
     const int n_qb = max(0, (sq + BM - 1) / BM - m_first);
-    const int total = G * n_qb;
 
     TileCopier<HD, BM, NT> qcp, ocp;
     qcp.init(qrs, wave, lane);
     ocp.init(dors, wave, lane);
     // Copy (q-head, query block) j into stage st.  Rows past the sequence
     // re-read its last row (finite values; their P and dS are zeroed below).
-    auto issue = [&](int j, int st) {
-        const int hq = hk * G + j / n_qb;
-        const int q0 = (m_first + j % n_qb) * BM;
-        char *qt = smem + st * C::STAGE;
-        char *ot = qt + C::QTILE;
-        char *lf = ot + C::QTILE;
-        const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hq);
-        const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hq);
+    // Copy block i of q-head hk * G + hidx into stage st.  Rows past the
+    // sequence re-read its last row (finite values; their P and dS are zeroed
+    // below).  Head pointers and LDS addresses are plain offsets, so a copy
+    // costs a few scalar adds besides the copies themselves.
+    const f16 *q_head0 = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hk * G);
+    const f16 *do_head0 = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hk * G);
+    const float *lse2_0 = a.dsum + int64_t(a.batch) * a.nheads * a.lse_seqlen +
+                          (int64_t(b) * a.nheads + hk * G) * a.lse_seqlen;
+    const float *dsum_0 = a.dsum + (int64_t(b) * a.nheads + hk * G) * a.lse_seqlen;
+    const uint32_t smem_l = lds_addr(smem);
+    auto issue = [&](int hidx, int i, int st) {
+        const int q0 = (m_first + i) * BM;
+        const uint32_t qt_l = smem_l + st * C::STAGE, ot_l = qt_l + C::QTILE, lf_l = ot_l + C::QTILE;
+        const f16 *qp = q_head0 + int64_t(hidx) * a.q.head_stride;
+        const f16 *dop = do_head0 + int64_t(hidx) * a.dout.head_stride;
         if (q0 + BM <= sq) {
-            qcp.copy(qt, qp + int64_t(q0) * qrs, qrs);
-            ocp.copy(ot, dop + int64_t(q0) * dors, dors);
+            qcp.copy_to(qt_l, qp + int64_t(q0) * qrs, qrs);
+            ocp.copy_to(ot_l, dop + int64_t(q0) * dors, dors);
         } else {
+            char *qt = smem + st * C::STAGE;
             dma_tile<HD, BM, NT>(qt, qp, qrs, q0, sq - 1, wave, lane);
-            dma_tile<HD, BM, NT>(ot, dop, dors, q0, sq - 1, wave, lane);
+            dma_tile<HD, BM, NT>(qt + C::QTILE, dop, dors, q0, sq - 1, wave, lane);
         }
         // LSE*log2(e) (second plane of the dsum workspace) and D per query row.
-        const float *lse2 = a.dsum + int64_t(a.batch) * a.nheads * a.lse_seqlen;
-        const int64_t lrow = (int64_t(b) * a.nheads + hq) * a.lse_seqlen + min(q0 + lane, sq - 1);
-        if (wave == 0) g2l4(lse2 + lrow, lf);
-        if (wave == 1) g2l4(a.dsum + lrow, lf + BM * 4);
+        const int64_t lrow = int64_t(hidx) * a.lse_seqlen + min(q0 + lane, sq - 1);
+        if (wave == 0) g2l4_to(lse2_0 + lrow, lf_l);
+        if (wave == 1) g2l4_to(dsum_0 + lrow, lf_l + BM * 4);
     };
 
     // The wave's 32-query half of block j: S = Q K^T and dP = dO V^T, P, dS,
@@ -421,11 +427,21 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     // block (masked).  Straight loops keep the dK/dV accumulators in place;
     // branching per block would copy them at every join.  Keys past the
     // sequence need no mask: their columns are never stored.
-    auto step = [&](int j, auto mask_tag, bool compute) {
+    // Each wave walks the same sequence of blocks (one barrier per block) in
+    // four straight loops per q-head: blocks whose half sees none of its keys
+    // (skipped), diagonal blocks (masked), full blocks, and a ragged last
+    // block (masked).  Straight loops keep the dK/dV accumulators in place;
+    // branching per block would copy them at every join.  Keys past the
+    // sequence need no mask: their columns are never stored.
+    int j = 0;  // running block index (stage j & 1)
+    auto step = [&](int hidx, int i, auto mask_tag, bool compute) {
         wait_vmem();
         __syncthreads();  // block j is in LDS; every wave is done with stage (j & 1) ^ 1
-        if (j + 1 < total) issue(j + 1, (j & 1) ^ 1);
-        if (compute) block(j, (m_first + j % n_qb) * BM + 32 * half, mask_tag);
+        const bool wrap = i + 1 == n_qb;  // the next block starts the next q-head
+        const int nh = wrap ? hidx + 1 : hidx, ni = wrap ? 0 : i + 1;
+        if (nh < G) issue(nh, ni, (j & 1) ^ 1);
+        if (compute) block(j, (m_first + i) * BM + 32 * half, mask_tag);
+        ++j;
     };
     auto clampi = [](int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); };
     // Smallest block index i whose half start (m_first + i) * BM + 32 * half reaches x.
@@ -434,12 +450,12 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     const int i1 = CAUSAL ? clampi(first_at(kw0 - 31 - causal_off), 0, n_qb) : 0;
     const int i2 = CAUSAL ? clampi(first_at(kw0 + 31 - causal_off), i1, n_qb) : 0;
     const int i3 = clampi(first_at(sq - 31), i2, n_qb);
-    if (total > 0) issue(0, 0);
-    for (int base = 0; base < total; base += n_qb) {
-        for (int i = 0; i < i1; ++i) step(base + i, std::true_type{}, false);
-        for (int i = i1; i < i2; ++i) step(base + i, std::true_type{}, true);
-        for (int i = i2; i < i3; ++i) step(base + i, std::false_type{}, true);
-        for (int i = i3; i < n_qb; ++i) step(base + i, std::true_type{}, true);
+    if (n_qb > 0) issue(0, 0, 0);
+    for (int hidx = 0; hidx < G && n_qb > 0; ++hidx) {
+        for (int i = 0; i < i1; ++i) step(hidx, i, std::true_type{}, false);
+        for (int i = i1; i < i2; ++i) step(hidx, i, std::true_type{}, true);
+        for (int i = i2; i < i3; ++i) step(hidx, i, std::false_type{}, true);
+        for (int i = i3; i < n_qb; ++i) step(hidx, i, std::true_type{}, true);
     }
 
     // Partial sums: half 1 hands over its dK, half 0 its dV (lane-contiguous

@@ -135,6 +135,66 @@ __device__ __forceinline__ void g2l16(const void *g, char *lds_base) {
         : "v"(g), "s"(l)
         : "memory");
 }
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const char *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char *)p;
+}
+// N (1, 2 or 4) global_load_lds_dwordx4 copies with one M0 save / restore:
+// copy i moves lane l's 16 bytes at g[i] to LDS byte l[i] + 16*l, where l[i]
+// are wave-uniform LDS addresses.  Same waiting rules as g2l16.
+template <int N>
+__device__ __forceinline__ void g2l16_batch(const void *const (&g)[N], const uint32_t (&l)[N]) {
+    uint32_t saved;
+    if constexpr (N == 1) {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %2\n\t"
+            "global_load_lds_dwordx4 %1, off\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "v"(g[0]), "s"(l[0])
+            : "memory");
+    } else if constexpr (N == 2) {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %3\n\t"
+            "global_load_lds_dwordx4 %1, off\n\t"
+            "s_mov_b32 m0, %4\n\t"
+            "global_load_lds_dwordx4 %2, off\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "v"(g[0]), "v"(g[1]), "s"(l[0]), "s"(l[1])
+            : "memory");
+    } else {
+        static_assert(N == 4, "batches of 1, 2 or 4 copies");
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %5\n\t"
+            "global_load_lds_dwordx4 %1, off\n\t"
+            "s_mov_b32 m0, %6\n\t"
+            "global_load_lds_dwordx4 %2, off\n\t"
+            "s_mov_b32 m0, %7\n\t"
+            "global_load_lds_dwordx4 %3, off\n\t"
+            "s_mov_b32 m0, %8\n\t"
+            "global_load_lds_dwordx4 %4, off\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "v"(g[0]), "v"(g[1]), "v"(g[2]), "v"(g[3]), "s"(l[0]), "s"(l[1]), "s"(l[2]), "s"(l[3])
+            : "memory");
+    }
+}
+// global_load_lds_dword to a wave-uniform LDS byte address l: lane l's 4 bytes land at l + 4*lane.
+__device__ __forceinline__ void g2l4_to(const void *g, uint32_t l) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(__builtin_amdgcn_readfirstlane(l))
+        : "memory");
+}
 // global_load_lds_dword: lane l's 4 bytes at `g` land at lds_base + 4*l.
 __device__ __forceinline__ void g2l4(const void *g, char *lds_base) {
     const uint32_t l =
@@ -236,10 +296,27 @@ struct TileCopier {
         goff = int64_t(row) * rs + 8 * (cs ^ swz<KCH>(row));
         lds0 = wave * 64 * 16;
     }
-    // src_row0: element pointer of the tile's first row (wave-uniform).
+    // src_row0: element pointer of the tile's first row (wave-uniform).  The
+    // copies go out as one batch (one M0 save / restore, LDS addresses as
+    // scalar offsets of the tile's base).
     __device__ __forceinline__ void copy(char *tile, const f16 *src_row0, int64_t rs) const {
+        copy_to(lds_addr(tile), src_row0, rs);
+    }
+    // The same with the tile given as its LDS byte address (no pointer cast in the loop).
+    __device__ __forceinline__ void copy_to(uint32_t tile_l, const f16 *src_row0, int64_t rs) const {
+        const uint32_t l0 = __builtin_amdgcn_readfirstlane(tile_l + lds0);
+        if constexpr (CPT == 1 || CPT == 2 || CPT == 4) {
+            const void *g[CPT];
+            uint32_t l[CPT];
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) g2l16(src_row0 + goff + int64_t(i) * RSTEP * rs, tile + lds0 + i * WAVES * 1024);
+            for (int i = 0; i < CPT; ++i) {
+                g[i] = src_row0 + goff + int64_t(i) * RSTEP * rs;
+                l[i] = l0 + i * WAVES * 1024;
+            }
+            g2l16_batch<CPT>(g, l);
+        } else {
+            static_assert(CPT == 1 || CPT == 2 || CPT == 4, "copies per lane");
+        }
     }
 };
 

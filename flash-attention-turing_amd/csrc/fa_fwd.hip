@@ -128,12 +128,13 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(co
     vcp.init(vrs, wave, lane);
     // Copy of key block nb into stage st.  A block that runs past the
     // sequence re-reads its last key for the missing rows (masked below).
+    const uint32_t smem_l = lds_addr(smem);
     auto issue = [&](int nb, int st) {
         char *ks = smem + st * C::STAGE;
         const int n0 = nb * BN;
         if (n0 + BN <= sk) {
-            kcp.copy(ks, kp + int64_t(n0) * krs, krs);
-            vcp.copy(ks + C::TILE, vp + int64_t(n0) * vrs, vrs);
+            kcp.copy_to(smem_l + st * C::STAGE, kp + int64_t(n0) * krs, krs);
+            vcp.copy_to(smem_l + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
         } else {
             dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
             dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
