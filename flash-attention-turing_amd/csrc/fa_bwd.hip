@@ -308,33 +308,45 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     ocp.init(dors, wave, lane);
     // Copy (q-head, query block) j into stage st.  Rows past the sequence
     // re-read its last row (finite values; their P and dS are zeroed below).
-    // Copy block i of q-head hk * G + hidx into stage st.  Rows past the
-    // sequence re-read its last row (finite values; their P and dS are zeroed
-    // below).  Head pointers and LDS addresses are plain offsets, so a copy
-    // costs a few scalar adds besides the copies themselves.
-    const f16 *q_head0 = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hk * G);
-    const f16 *do_head0 = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hk * G);
-    const float *lse2_0 = a.dsum + int64_t(a.batch) * a.nheads * a.lse_seqlen +
-                          (int64_t(b) * a.nheads + hk * G) * a.lse_seqlen;
-    const float *dsum_0 = a.dsum + (int64_t(b) * a.nheads + hk * G) * a.lse_seqlen;
+    // Copies of the next block: running pointers to its first Q / dO row and
+    // its LSE / D entries, advanced by one block per step (and moved to the
+    // next q-head of the group after the last block of a head), so a step's
+    // address work is a few scalar adds.  Rows past the sequence re-read its
+    // last row (finite values; their P and dS are zeroed below).
+    const int64_t lse_plane = int64_t(a.batch) * a.nheads * a.lse_seqlen;
+    const f16 *nq = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, hk * G);
+    const f16 *ndo = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, hk * G);
+    const float *nd = a.dsum + (int64_t(b) * a.nheads + hk * G) * a.lse_seqlen;
+    int nh = 0, ni = 0;  // q-head (within the group) and block of the next copy
     const uint32_t smem_l = lds_addr(smem);
-    auto issue = [&](int hidx, int i, int st) {
-        const int q0 = (m_first + i) * BM;
+    const int64_t q_step = int64_t(BM) * qrs, do_step = int64_t(BM) * dors;
+    const f16 *nq_row = nq + int64_t(m_first) * q_step, *ndo_row = ndo + int64_t(m_first) * do_step;
+    auto issue_next = [&](int st) {
+        const int q0 = (m_first + ni) * BM;
         const uint32_t qt_l = smem_l + st * C::STAGE, ot_l = qt_l + C::QTILE, lf_l = ot_l + C::QTILE;
-        const f16 *qp = q_head0 + int64_t(hidx) * a.q.head_stride;
-        const f16 *dop = do_head0 + int64_t(hidx) * a.dout.head_stride;
         if (q0 + BM <= sq) {
-            qcp.copy_to(qt_l, qp + int64_t(q0) * qrs, qrs);
-            ocp.copy_to(ot_l, dop + int64_t(q0) * dors, dors);
+            qcp.copy_to(qt_l, nq_row, qrs);
+            ocp.copy_to(ot_l, ndo_row, dors);
         } else {
             char *qt = smem + st * C::STAGE;
-            dma_tile<HD, BM, NT>(qt, qp, qrs, q0, sq - 1, wave, lane);
-            dma_tile<HD, BM, NT>(qt + C::QTILE, dop, dors, q0, sq - 1, wave, lane);
+            dma_tile<HD, BM, NT>(qt, nq, qrs, q0, sq - 1, wave, lane);
+            dma_tile<HD, BM, NT>(qt + C::QTILE, ndo, dors, q0, sq - 1, wave, lane);
         }
         // LSE*log2(e) (second plane of the dsum workspace) and D per query row.
-        const int64_t lrow = int64_t(hidx) * a.lse_seqlen + min(q0 + lane, sq - 1);
-        if (wave == 0) g2l4_to(lse2_0 + lrow, lf_l);
-        if (wave == 1) g2l4_to(dsum_0 + lrow, lf_l + BM * 4);
+        const int r = min(q0 + lane, sq - 1);
+        if (wave == 0) g2l4_to(nd + lse_plane + r, lf_l);
+        if (wave == 1) g2l4_to(nd + r, lf_l + BM * 4);
+        nq_row += q_step;
+        ndo_row += do_step;
+        if (++ni == n_qb) {
+            ni = 0;
+            ++nh;
+            nq += a.q.head_stride;
+            ndo += a.dout.head_stride;
+            nd += a.lse_seqlen;
+            nq_row = nq + int64_t(m_first) * q_step;
+            ndo_row = ndo + int64_t(m_first) * do_step;
+        }
     };
 
     // The wave's 32-query half of block j: S = Q K^T and dP = dO V^T, P, dS,
@@ -434,12 +446,10 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     // branching per block would copy them at every join.  Keys past the
     // sequence need no mask: their columns are never stored.
     int j = 0;  // running block index (stage j & 1)
-    auto step = [&](int hidx, int i, auto mask_tag, bool compute) {
+    auto step = [&](int i, auto mask_tag, bool compute) {
         wait_vmem();
         __syncthreads();  // block j is in LDS; every wave is done with stage (j & 1) ^ 1
-        const bool wrap = i + 1 == n_qb;  // the next block starts the next q-head
-        const int nh = wrap ? hidx + 1 : hidx, ni = wrap ? 0 : i + 1;
-        if (nh < G) issue(nh, ni, (j & 1) ^ 1);
+        if (nh < G) issue_next((j & 1) ^ 1);
         if (compute) block(j, (m_first + i) * BM + 32 * half, mask_tag);
         ++j;
     };
@@ -450,12 +460,12 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     const int i1 = CAUSAL ? clampi(first_at(kw0 - 31 - causal_off), 0, n_qb) : 0;
     const int i2 = CAUSAL ? clampi(first_at(kw0 + 31 - causal_off), i1, n_qb) : 0;
     const int i3 = clampi(first_at(sq - 31), i2, n_qb);
-    if (n_qb > 0) issue(0, 0, 0);
+    if (n_qb > 0) issue_next(0);
     for (int hidx = 0; hidx < G && n_qb > 0; ++hidx) {
-        for (int i = 0; i < i1; ++i) step(hidx, i, std::true_type{}, false);
-        for (int i = i1; i < i2; ++i) step(hidx, i, std::true_type{}, true);
-        for (int i = i2; i < i3; ++i) step(hidx, i, std::false_type{}, true);
-        for (int i = i3; i < n_qb; ++i) step(hidx, i, std::true_type{}, true);
+        for (int i = 0; i < i1; ++i) step(i, std::true_type{}, false);
+        for (int i = i1; i < i2; ++i) step(i, std::true_type{}, true);
+        for (int i = i2; i < i3; ++i) step(i, std::false_type{}, true);
+        for (int i = i3; i < n_qb; ++i) step(i, std::true_type{}, true);
     }
 
     // Partial sums: half 1 hands over its dK, half 0 its dV (lane-contiguous
