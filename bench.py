@@ -109,7 +109,7 @@ def train_step_setup(batch, seqlen, heads, hd, seed, device):
     o = torch.empty_like(q)
     lse = torch.empty((batch, heads, seqlen), dtype=torch.float32, device=device)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=device)  # D, LSE*log2(e)
+    dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=device)  # -D, LSE*log2(e)
     scale = hd ** -0.5
     fa = fa_capi.fwd_args(q, k, v, o, lse, scale, True)
     ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, True)

@@ -27,7 +27,8 @@ namespace fa {
 constexpr int kBwdThreads = 256;
 
 // ---------------------------------------------------------------------------
-// Preprocess: dsum[b][h][i] = sum_d fp32(O) * fp32(dO); padding rows get 0.
+// Preprocess: dsum[b][h][i] = -sum_d fp32(O) * fp32(dO) (stored negated, the
+// initial value of the dK/dV kernel's dP accumulators); padding rows get 0.
 // One group of KCH threads per row; consecutive groups take consecutive rows of
 // one head so the row sums are written contiguously.  fa_bwd computes the same
 // sums inside the dQ kernel; this standalone kernel serves fa_bwd_preprocess.
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a
     if (c == 0) {
         const int64_t idx = (int64_t(b) * a.nheads + h) * a.lse_seqlen + i;
         const int64_t plane = int64_t(a.batch) * a.nheads * a.lse_seqlen;
-        a.dsum[idx] = acc;
+        a.dsum[idx] = -acc;
         a.dsum[plane + idx] = i < si.sq ? a.lse[idx] * kLog2e : 0.f;
     }
 }
@@ -65,7 +66,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a
 // V copied HBM -> LDS (two stages, global_load_lds); S^T = K Q^T and
 // dP^T = V dO^T read K, V as natural A operands, dQ^T += K^T dS^T reads K
 // transposed (ds_read_b64_tr_b16).  The prologue computes D = rowsum(dO * O)
-// for the workgroup's rows and stores it for the dK/dV kernel.
+// for the workgroup's rows and stores -D for the dK/dV kernel.
 template <int HD>
 struct DqCfg {
     static constexpr int BM = 128, BN = 64, NT = kBwdThreads;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     const float dsum = dpart + __shfl_xor(dpart, 32);
     const float lse2 = qv ? a.lse[lrow + qi] * kLog2e : 0.f;
     if (qv && hh == 0) {
-        a.dsum[lrow + qi] = dsum;
+        a.dsum[lrow + qi] = -dsum;  // -D: the dK/dV kernel seeds its dP accumulators with it
         a.dsum[int64_t(a.batch) * a.nheads * a.lse_seqlen + lrow + qi] = lse2;  // for the dK/dV kernel
     }
     wait_vmem();  // only the tile copies are in flight inside the loop
@@ -377,7 +378,20 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < PIPE - 1; ++g) ld(g);
-        f32x16 s = zero16(), dp = zero16();
+        // dP starts from -D of its rows (the workspace holds -D), so the
+        // product comes out as dP - D.
+        f32x16 s = zero16(), dp;
+#pragma unroll
+        for (int r8 = 0; r8 < 2; ++r8) {
+            const int ql0 = r0 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
+            const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + BM + ql0);
+            const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + BM + ql0 + 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                dp[8 * r8 + u] = d_a[u];
+                dp[8 * r8 + 4 + u] = d_b[u];
+            }
+        }
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             if (g + PIPE - 1 < NG) ld(g + PIPE - 1);
@@ -390,13 +404,10 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
             const int ql0 = r0 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
             const f32x4 l_a = *reinterpret_cast<const f32x4 *>(lf + ql0);
             const f32x4 l_b = *reinterpret_cast<const f32x4 *>(lf + ql0 + 4);
-            const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + BM + ql0);
-            const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + BM + ql0 + 4);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int r = 8 * r8 + u;
                 const float l2 = u < 4 ? l_a[u] : l_b[u - 4];
-                const float dsum = u < 4 ? d_a[u] : d_b[u - 4];
                 float p = exp2_fast(fmaf(s[r], cs, -l2));
                 if constexpr (MASK) {
                     const int q = qh0 + 16 * r8 + 8 * hh + u;
@@ -404,7 +415,7 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
                     p = dead ? 0.f : p;
                 }
                 s[r] = p;
-                dp[r] = p * (dp[r] - dsum);
+                dp[r] = p * dp[r];
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -589,7 +600,7 @@ extern "C" int fa_bwd_dkdv(const fa_bwd_args *args, void *stream) {
 }
 
 extern "C" int fa_bwd(const fa_bwd_args *args, void *stream) {
-    // The dQ kernel also writes D = rowsum(dO * O) for the dK/dV kernel.
+    // The dQ kernel also writes -D = -rowsum(dO * O) for the dK/dV kernel.
     int rc = fa_bwd_dq(args, stream);
     if (rc) return rc;
     return fa_bwd_dkdv(args, stream);

@@ -75,7 +75,7 @@ typedef struct fa_bwd_args {
     fa_tensor q, k, v, o, dout;     /* fp16 inputs                               */
     fa_tensor dq, dk, dv;           /* fp16 outputs, every valid row written     */
     const float *lse;               /* fp32 [batch][nheads][lse_seqlen]          */
-    float *dsum;                    /* workspace fp32 [2][batch][nheads][lse_seqlen]: rowsum(dO*O),
+    float *dsum;                    /* workspace fp32 [2][batch][nheads][lse_seqlen]: -rowsum(dO*O),
                                        then LSE*log2(e) (written by fa_bwd_dq / fa_bwd_preprocess) */
     const int32_t *cu_seqlens_q;
     const int32_t *cu_seqlens_k;
@@ -85,7 +85,7 @@ typedef struct fa_bwd_args {
     int32_t causal;
 } fa_bwd_args;
 
-/* D = rowsum(dO * O) (flash_bwd_preprocess_kernel.h:23-96). */
+/* D = rowsum(dO * O) (flash_bwd_preprocess_kernel.h:23-96), stored negated in dsum plane 0. */
 int fa_bwd_preprocess(const fa_bwd_args *args, void *stream);
 /* dQ kernel (flash_bwd_kernel.h:25-609); computes and stores the dsum workspace itself. */
 int fa_bwd_dq(const fa_bwd_args *args, void *stream);
