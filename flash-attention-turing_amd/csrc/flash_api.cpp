@@ -40,10 +40,35 @@ inline void check_fp16_cuda(const at::Tensor &t, const char *name) {
 }
 
 // 16-byte aligned base and strides (in elements, multiple of 8), last dim contiguous.
-inline at::Tensor aligned(const at::Tensor &t) {
+inline bool is_aligned(const at::Tensor &t) {
     bool ok = t.stride(-1) == 1 && (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0;
     for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = (t.stride(i) % 8) == 0 || t.size(i) == 1;
-    return ok ? t : t.contiguous();
+    return ok;
+}
+inline at::Tensor aligned(const at::Tensor &t) { return is_aligned(t) ? t : t.contiguous(); }
+
+// A gradient output: the caller's tensor (for instance one slice of a packed
+// dqkv) when it is given, written in place if its layout suits the kernels and
+// through a temporary copied into it otherwise; a new tensor when absent.
+// zero: rows no sequence covers (varlen padding) read 0 in a new tensor.
+struct GradOut {
+    at::Tensor dst, buf;
+    void finish() {
+        if (!buf.is_same(dst)) dst.copy_(buf);
+    }
+};
+inline GradOut grad_out(const std::optional<at::Tensor> &given, const at::Tensor &like, bool zero,
+                        const char *name) {
+    auto fresh = [&] { return zero ? at::zeros(like.sizes(), like.options()) : at::empty(like.sizes(), like.options()); };
+    if (!given.has_value()) {
+        at::Tensor t = fresh();
+        return {t, t};
+    }
+    const at::Tensor &g = *given;
+    check_fp16_cuda(g, name);
+    TORCH_CHECK(g.device() == like.device(), name, " must be on the device of its input");
+    TORCH_CHECK(g.sizes() == like.sizes(), name, " must have the shape of its input");
+    return {g, is_aligned(g) ? g : fresh()};
 }
 
 inline fa_tensor desc4(const at::Tensor &t) {  // [batch][row][head][d]
@@ -111,7 +136,9 @@ std::vector<at::Tensor> mha_fwd(at::Tensor q, at::Tensor k, at::Tensor v, const 
 }
 
 std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor out, at::Tensor l,
-                                at::Tensor dout, const float softmax_scale, bool is_causal) {
+                                at::Tensor dout, const float softmax_scale, bool is_causal,
+                                std::optional<at::Tensor> dq_, std::optional<at::Tensor> dk_,
+                                std::optional<at::Tensor> dv_) {
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "q, k, v must be rank-4 tensors");
     TORCH_CHECK(out.dim() == 4 && dout.dim() == 4, "out and dout must be rank-4 tensors");
     const int64_t batch_size = q.size(0), seqlen_q = q.size(1), num_heads = q.size(2), head_size = q.size(3);
@@ -134,10 +161,8 @@ std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Te
     out = aligned(out);
     dout = aligned(dout);
 
-    at::Tensor dq = at::empty(q.sizes(), q.options());
-    at::Tensor dk = at::empty(k.sizes(), k.options());
-    at::Tensor dv = at::empty(v.sizes(), v.options());
-    at::Tensor dsum = at::empty({2, l.numel()}, l.options());  // D, then LSE*log2(e)
+    GradOut dq = grad_out(dq_, q, false, "dq"), dk = grad_out(dk_, k, false, "dk"), dv = grad_out(dv_, v, false, "dv");
+    at::Tensor dsum = at::empty({2, l.numel()}, l.options());  // -D, then LSE*log2(e)
 
     fa_bwd_args a{};
     a.q = desc4(q);
@@ -145,9 +170,9 @@ std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Te
     a.v = desc4(v);
     a.o = desc4(out);
     a.dout = desc4(dout);
-    a.dq = desc4(dq);
-    a.dk = desc4(dk);
-    a.dv = desc4(dv);
+    a.dq = desc4(dq.buf);
+    a.dk = desc4(dk.buf);
+    a.dv = desc4(dv.buf);
     a.lse = l.data_ptr<float>();
     a.dsum = dsum.data_ptr<float>();
     a.batch = int32_t(batch_size);
@@ -160,7 +185,8 @@ std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Te
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
     check_rc(fa_bwd(&a, current_stream()), "fa_bwd");
-    return {dq, dk, dv};
+    for (auto *g : {&dq, &dk, &dv}) g->finish();
+    return {dq.dst, dk.dst, dv.dst};
 }
 
 static void check_cu_seqlens(const at::Tensor &cu_seqlens_q, const at::Tensor &cu_seqlens_k) {
@@ -230,7 +256,8 @@ std::vector<at::Tensor> mha_varlen_fwd(at::Tensor q, at::Tensor k, at::Tensor v,
 std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor out, at::Tensor l,
                                        at::Tensor dout, at::Tensor cu_seqlens_q, at::Tensor cu_seqlens_k,
                                        const int max_seqlen_q, const int max_seqlen_k, const float softmax_scale,
-                                       bool is_causal) {
+                                       bool is_causal, std::optional<at::Tensor> dq_, std::optional<at::Tensor> dk_,
+                                       std::optional<at::Tensor> dv_) {
     TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "q, k, v must be rank-3 packed tensors");
     check_cu_seqlens(cu_seqlens_q, cu_seqlens_k);
     const int64_t batch_size = cu_seqlens_q.numel() - 1;
@@ -252,11 +279,10 @@ std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v,
     out = aligned(out);
     dout = aligned(dout);
 
-    // Packed rows past the last sequence belong to no sequence and stay 0.
-    at::Tensor dq = at::zeros(q.sizes(), q.options());
-    at::Tensor dk = at::zeros(k.sizes(), k.options());
-    at::Tensor dv = at::zeros(v.sizes(), v.options());
-    at::Tensor dsum = at::empty({2, l.numel()}, l.options());  // D, then LSE*log2(e)
+    // Packed rows past the last sequence belong to no sequence: 0 in a new
+    // gradient tensor, left as they are in a caller's.
+    GradOut dq = grad_out(dq_, q, true, "dq"), dk = grad_out(dk_, k, true, "dk"), dv = grad_out(dv_, v, true, "dv");
+    at::Tensor dsum = at::empty({2, l.numel()}, l.options());  // -D, then LSE*log2(e)
 
     fa_bwd_args a{};
     a.q = desc3(q);
@@ -264,9 +290,9 @@ std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v,
     a.v = desc3(v);
     a.o = desc3(out);
     a.dout = desc3(dout);
-    a.dq = desc3(dq);
-    a.dk = desc3(dk);
-    a.dv = desc3(dv);
+    a.dq = desc3(dq.buf);
+    a.dk = desc3(dk.buf);
+    a.dv = desc3(dv.buf);
     a.lse = l.data_ptr<float>();
     a.dsum = dsum.data_ptr<float>();
     a.cu_seqlens_q = cu_seqlens_q.data_ptr<int32_t>();
@@ -281,7 +307,8 @@ std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v,
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
     check_rc(fa_bwd(&a, current_stream()), "fa_bwd (varlen)");
-    return {dq, dk, dv};
+    for (auto *g : {&dq, &dk, &dv}) g->finish();
+    return {dq.dst, dk.dst, dv.dst};
 }
 
 std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
@@ -480,8 +507,15 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("fwd", &mha_fwd, "Forward pass");
-    m.def("bwd", &mha_bwd, "Backward pass");
+    // dq / dk / dv (optional, after the reference's arguments): tensors the
+    // gradients are written into, such as the slices of a packed dqkv.
+    m.def("bwd", &mha_bwd, "Backward pass", py::arg("q"), py::arg("k"), py::arg("v"), py::arg("out"), py::arg("l"),
+          py::arg("dout"), py::arg("softmax_scale"), py::arg("is_causal"), py::arg("dq") = py::none(),
+          py::arg("dk") = py::none(), py::arg("dv") = py::none());
     m.def("varlen_fwd", &mha_varlen_fwd, "Varlen forward pass");
-    m.def("varlen_bwd", &mha_varlen_bwd, "Varlen backward pass");
+    m.def("varlen_bwd", &mha_varlen_bwd, "Varlen backward pass", py::arg("q"), py::arg("k"), py::arg("v"),
+          py::arg("out"), py::arg("l"), py::arg("dout"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_k"),
+          py::arg("max_seqlen_q"), py::arg("max_seqlen_k"), py::arg("softmax_scale"), py::arg("is_causal"),
+          py::arg("dq") = py::none(), py::arg("dk") = py::none(), py::arg("dv") = py::none());
     m.def("fwd_kvcache", &mha_fwd_kvcache, "KV-cache forward pass");
 }

@@ -44,9 +44,10 @@ def _flash_attn_forward(q, k, v, softmax_scale: float, causal: bool):
     return out, lse
 
 
-def _flash_attn_backward(dout, q, k, v, out, lse, softmax_scale: float, causal: bool):
+def _flash_attn_backward(dout, q, k, v, out, lse, softmax_scale: float, causal: bool, dq=None, dk=None, dv=None):
+    """dq / dk / dv, when given, are written in place (e.g. slices of a packed dqkv) and returned."""
     dout, q, k, v, out, lse = (maybe_contiguous(t) for t in (dout, q, k, v, out, lse))
-    dq, dk, dv = flash_attn_gpu.bwd(q, k, v, out, lse, dout, softmax_scale, causal)
+    dq, dk, dv = flash_attn_gpu.bwd(q, k, v, out, lse, dout, softmax_scale, causal, dq, dk, dv)
     return dq, dk, dv
 
 
@@ -73,10 +74,15 @@ def _flash_attn_varlen_backward(
     max_seqlen_k: int,
     softmax_scale: float,
     causal: bool,
+    dq=None,
+    dk=None,
+    dv=None,
 ):
+    """dq / dk / dv, when given, are written in place (rows no sequence covers are left as they are)."""
     dout, q, k, v, out, lse = (maybe_contiguous(t) for t in (dout, q, k, v, out, lse))
     dq, dk, dv = flash_attn_gpu.varlen_bwd(
-        q, k, v, out, lse, dout, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal
+        q, k, v, out, lse, dout, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
+        dq, dk, dv,
     )
     return dq, dk, dv
 
@@ -126,12 +132,21 @@ class FlashAttnFunc(torch.autograd.Function):
         return dq, dk, dv, None, None, None
 
 
+# Packed inputs: the kernels take row and head strides, so q / k / v are
+# passed as views of the packed tensor (no copies, unlike the reference's
+# interface.py:208-212, 244-247), and the backward writes the gradient slices
+# straight into one packed gradient (no torch.stack, interface.py:226-231).
+
+
 def _unpack(packed: torch.Tensor, dim: int, n: int):
-    return tuple(packed.select(dim=dim, index=i).contiguous() for i in range(n))
+    return tuple(packed.select(dim=dim, index=i) for i in range(n))
 
 
-def _repack(parts, dim: int) -> torch.Tensor:
-    return torch.stack(parts, dim=dim)
+def _packed_grad(packed, dim: int, zero: bool):
+    """A gradient for a packed input (shape, dtype, device) and its slices along dim."""
+    shape, dtype, device = packed
+    g = (torch.zeros if zero else torch.empty)(shape, dtype=dtype, device=device)
+    return g, tuple(g.select(dim=dim, index=i) for i in range(shape[dim]))
 
 
 class FlashAttnQKVPackedFunc(torch.autograd.Function):
@@ -142,14 +157,16 @@ class FlashAttnQKVPackedFunc(torch.autograd.Function):
         out, lse = _flash_attn_forward(q, k, v, softmax_scale, causal)
         if is_grad_enabled and qkv.requires_grad:
             ctx.save_for_backward(q, k, v, out, lse)
+            ctx.packed = (qkv.shape, qkv.dtype, qkv.device)
             ctx.softmax_scale, ctx.causal = softmax_scale, causal
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal)
-        return _repack((dq, dk, dv), 2), None, None, None
+        dqkv, (dq, dk, dv) = _packed_grad(ctx.packed, 2, False)
+        _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal, dq, dk, dv)
+        return dqkv, None, None, None
 
 
 class FlashAttnKVPackedFunc(torch.autograd.Function):
@@ -160,14 +177,16 @@ class FlashAttnKVPackedFunc(torch.autograd.Function):
         out, lse = _flash_attn_forward(q, k, v, softmax_scale, causal)
         if is_grad_enabled and (q.requires_grad or kv.requires_grad):
             ctx.save_for_backward(q, k, v, out, lse)
+            ctx.packed = (kv.shape, kv.dtype, kv.device)
             ctx.softmax_scale, ctx.causal = softmax_scale, causal
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal)
-        return dq, _repack((dk, dv), 2), None, None, None
+        dkv, (dk, dv) = _packed_grad(ctx.packed, 2, False)
+        dq, _, _ = _flash_attn_backward(dout, q, k, v, out, lse, ctx.softmax_scale, ctx.causal, None, dk, dv)
+        return dq, dkv, None, None, None
 
 
 class FlashAttnVarlenFunc(torch.autograd.Function):
@@ -204,6 +223,7 @@ class FlashAttnVarlenQKVPackedFunc(torch.autograd.Function):
         )
         if is_grad_enabled and qkv.requires_grad:
             ctx.save_for_backward(q, k, v, out, lse, cu_seqlens)
+            ctx.packed = (qkv.shape, qkv.dtype, qkv.device)
             ctx.max_seqlen = max_seqlen
             ctx.softmax_scale, ctx.causal = softmax_scale, causal
         return out
@@ -211,11 +231,12 @@ class FlashAttnVarlenQKVPackedFunc(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse, cu_seqlens = ctx.saved_tensors
-        dq, dk, dv = _flash_attn_varlen_backward(
+        dqkv, (dq, dk, dv) = _packed_grad(ctx.packed, 1, True)
+        _flash_attn_varlen_backward(
             dout, q, k, v, out, lse, cu_seqlens, cu_seqlens, ctx.max_seqlen, ctx.max_seqlen,
-            ctx.softmax_scale, ctx.causal,
+            ctx.softmax_scale, ctx.causal, dq, dk, dv,
         )
-        return _repack((dq, dk, dv), 1), None, None, None, None, None
+        return dqkv, None, None, None, None, None
 
 
 class FlashAttnVarlenKVPackedFunc(torch.autograd.Function):
@@ -229,6 +250,7 @@ class FlashAttnVarlenKVPackedFunc(torch.autograd.Function):
         )
         if is_grad_enabled and (q.requires_grad or kv.requires_grad):
             ctx.save_for_backward(q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k)
+            ctx.packed = (kv.shape, kv.dtype, kv.device)
             ctx.max_seqlen_q, ctx.max_seqlen_k = max_seqlen_q, max_seqlen_k
             ctx.softmax_scale, ctx.causal = softmax_scale, causal
         return out
@@ -236,11 +258,12 @@ class FlashAttnVarlenKVPackedFunc(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
-        dq, dk, dv = _flash_attn_varlen_backward(
+        dkv, (dk, dv) = _packed_grad(ctx.packed, 1, True)
+        dq, _, _ = _flash_attn_varlen_backward(
             dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
-            ctx.softmax_scale, ctx.causal,
+            ctx.softmax_scale, ctx.causal, None, dk, dv,
         )
-        return dq, _repack((dk, dv), 1), None, None, None, None, None, None, None
+        return dq, dkv, None, None, None, None, None, None, None
 
 
 # ---------------------------------------------------------------------------

@@ -79,3 +79,45 @@ def test_bwd_deterministic(device):
         res.append([t.grad.clone() for t in (q, k, v)])
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_kvpacked_bwd_matches_unpacked(device):
+    # GQA kv packed (b, s, 2, hk, d): dkv is one tensor written slice by slice.
+    g = torch.Generator().manual_seed(23)
+    q = randn16((2, 150, 4, 128), g).to(device).requires_grad_()
+    kv = randn16((2, 170, 2, 2, 128), g).to(device).requires_grad_()
+    do = randn16((2, 150, 4, 128), g).to(device)
+    fai.flash_attn_kvpacked_func(q, kv, causal=True).backward(do)
+    qr = q.detach().clone().requires_grad_()
+    k, v = (kv.detach()[:, :, i].clone().requires_grad_() for i in range(2))
+    fai.flash_attn_func(qr, k, v, causal=True).backward(do)
+    assert torch.equal(q.grad, qr.grad)
+    assert torch.equal(kv.grad[:, :, 0], k.grad)
+    assert torch.equal(kv.grad[:, :, 1], v.grad)
+
+
+@pytest.mark.gpu
+def test_bwd_into_given_tensors(device):
+    # Gradients written into caller tensors: strided slices in place (same
+    # storage returned), and a view whose base is not 16-byte aligned through
+    # a temporary; both equal the freshly allocated result.
+    g = torch.Generator().manual_seed(24)
+    q, k, v = (randn16((1, 96, 2, 64), g).to(device) for _ in range(3))
+    do = randn16((1, 96, 2, 64), g).to(device)
+    s = 64 ** -0.5
+    out, lse = fai._flash_attn_forward(q, k, v, s, True)
+    ref = fai._flash_attn_backward(do, q, k, v, out, lse, s, True)
+    packed = torch.full((1, 96, 3, 2, 64), 7.0, dtype=torch.float16, device=device)
+    views = tuple(packed[:, :, i] for i in range(3))
+    got = fai._flash_attn_backward(do, q, k, v, out, lse, s, True, *views)
+    for r, x, w in zip(ref, got, views):
+        assert x.data_ptr() == w.data_ptr()
+        assert torch.equal(x, r)
+    buf = torch.zeros(1 * 96 * 2 * 64 + 4, dtype=torch.float16, device=device)
+    odd = buf[4:].view(1, 96, 2, 64)  # base 8 bytes past a 16-byte boundary
+    dq, _, _ = fai._flash_attn_backward(do, q, k, v, out, lse, s, True, odd, None, None)
+    assert dq.data_ptr() == odd.data_ptr() and torch.equal(dq, ref[0])
+    assert torch.equal(buf[:4], torch.zeros(4, dtype=torch.float16, device=device))
+    with pytest.raises(RuntimeError, match="dk must have the shape of its input"):
+        fai._flash_attn_backward(do, q, k, v, out, lse, s, True, None, views[1][:, :50], None)

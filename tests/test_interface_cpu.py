@@ -175,3 +175,15 @@ def test_extension_rejects_cpu_tensors_with_reference_messages():
             _t(1, 1, 2, 64), _t(1, 8, 2, 64), _t(1, 8, 2, 64), None, None, torch.zeros(1, dtype=torch.int32),
             None, None, None, None, None, None, _t(1, 1, 2, 64), 0.1, True, -1, -1, 0.0, True, 0,
         )
+
+
+def test_packed_inputs_are_views():
+    # The packed wrappers hand the kernels strided views of the packed tensor
+    # (no copies); the gradient helper returns one packed tensor and its slices.
+    qkv = _t(2, 5, 3, 4, 64, dtype=torch.float16)
+    parts = fai._unpack(qkv, 2, 3)
+    for i, t in enumerate(parts):
+        assert t.data_ptr() == qkv[:, :, i].data_ptr() and t.stride() == qkv[:, :, i].stride()
+    g, (a, b) = fai._packed_grad((torch.Size([7, 2, 3, 64]), torch.float16, torch.device("cpu")), 1, True)
+    assert g.shape == (7, 2, 3, 64) and not g.any()
+    assert a.data_ptr() == g[:, 0].data_ptr() and b.data_ptr() == g[:, 1].data_ptr()

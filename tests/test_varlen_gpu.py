@@ -75,3 +75,26 @@ def test_varlen_public_packed_variants(device):
     assert torch.equal(out_p, out)
     out_kv = fai.flash_attn_varlen_kvpacked_func(q, qkv[:, 1:], cu, cu, max(lens), max(lens), causal=True)
     assert torch.equal(out_kv, out)
+
+
+@pytest.mark.gpu
+def test_varlen_packed_bwd_matches_unpacked(device):
+    # Packed varlen gradients (one dqkv / dkv written slice by slice; rows past
+    # the last sequence read 0) equal the unpacked path's, bit for bit.
+    g = torch.Generator().manual_seed(32)
+    lens = [100, 37, 260]
+    cu = cu_from_lengths(lens).to(device)
+    total = sum(lens) + 5  # 5 packed rows no sequence covers
+    qkv = randn16((total, 3, 4, 64), g).to(device).requires_grad_()
+    do = randn16((total, 4, 64), g).to(device)
+    fai.flash_attn_varlen_qkvpacked_func(qkv, cu, max(lens), causal=True).backward(do)
+    q, k, v = (qkv.detach()[:, i].clone().requires_grad_() for i in range(3))
+    fai.flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal=True).backward(do)
+    for i, t in enumerate((q, k, v)):
+        assert torch.equal(qkv.grad[:, i], t.grad)
+    assert not qkv.grad[sum(lens):].any()
+    q2 = q.detach().clone().requires_grad_()
+    kv = qkv.detach()[:, 1:].clone().requires_grad_()
+    fai.flash_attn_varlen_kvpacked_func(q2, kv, cu, cu, max(lens), max(lens), causal=True).backward(do)
+    assert torch.equal(q2.grad, q.grad)
+    assert torch.equal(kv.grad[:, 0], k.grad) and torch.equal(kv.grad[:, 1], v.grad)
