@@ -78,7 +78,21 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(co
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
     const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k,
                                 a.seqused_k_add);
-    const int sq = si.sq, sk = si.sk;
+    const int sq = si.sq;
+    int sk = si.sk;
+    int kb = a.k_batch_idx ? a.k_batch_idx[b] : b;
+    if (a.seqused_k) {
+        // KV-cache chunk: a key count past the cache or a cache row outside it
+        // leaves the batch with no keys, and the error goes to the status word.
+        const int used = a.seqused_k[b];
+        const int err = (used < 0 || int64_t(used) + a.seqused_k_add > a.seqlen_k ? 1 : 0) |
+                        (a.k_batch_idx && a.k_batch > 0 && (kb < 0 || kb >= a.k_batch) ? 2 : 0);
+        if (err) {
+            sk = 0;
+            kb = 0;
+            if (a.status && tid == 0) atomicOr(a.status, err);
+        }
+    }
     const int m0 = mb * BM;
     float *lse_row = a.lse + (int64_t(b) * a.nheads + h) * a.lse_seqlen;
     if (m0 >= sq) {
@@ -86,7 +100,6 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(co
         for (int i = m0 + tid; i < m0 + BM && i < a.lse_seqlen; i += NT) lse_row[i] = 0.f;
         return;
     }
-    const int kb = a.k_batch_idx ? a.k_batch_idx[b] : b;
     const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, h);
     const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, kb, si.k_start, hk);
     const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, kb, si.k_start, hk);

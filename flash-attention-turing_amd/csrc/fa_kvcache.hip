@@ -56,6 +56,30 @@ __device__ __forceinline__ const f16 *kv_row_ptr(const fa_tensor &t, const fa_kv
     return (const f16 *)t.ptr + off + int64_t(hk) * t.head_stride;
 }
 
+// Cache length and cache row of sequence b, checked against the cache: a
+// negative length, more tokens than the cache holds after the append, or a
+// row outside a remapped cache makes the sequence invalid (err bit 1:
+// capacity, bit 2: row).  An invalid sequence is not appended to and is
+// attended over no keys, so no access leaves the cache whatever the lengths
+// and indices hold; the host learns of it from the status word.
+struct KvSeq {
+    int L0;   // tokens in the cache before the append (0 when invalid)
+    int row;  // cache row (contiguous cache)
+    int err;
+};
+__device__ __forceinline__ KvSeq kv_seq(const fa_kvcache_args &a, int b) {
+    KvSeq s;
+    s.L0 = a.cache_seqlens[b];
+    s.row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
+    s.err = (s.L0 < 0 || (a.cache_capacity > 0 && int64_t(s.L0) + a.seqlen_new > a.cache_capacity) ? 1 : 0) |
+            (a.cache_batch_idx && a.cache_batch > 0 && (s.row < 0 || s.row >= a.cache_batch) ? 2 : 0);
+    if (s.err) {
+        s.L0 = 0;
+        s.row = 0;
+    }
+    return s;
+}
+
 // ---------------------------------------------------------------------------
 // Append: one thread per 16-byte chunk of k_new / v_new.
 template <int HD>
@@ -70,8 +94,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a)
     rest /= a.nheads_k;
     const int t = int(rest % a.seqlen_new);
     const int b = int(rest / a.seqlen_new);
-    const int pos = a.cache_seqlens[b] + t;
-    const int cache_row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
+    const KvSeq sq = kv_seq(a, b);
+    if (sq.err) {
+        if (a.status && idx % (int64_t(a.seqlen_new) * a.nheads_k * KCH) == 0) atomicOr(a.status, sq.err);
+        return;
+    }
+    const int pos = sq.L0 + t;
+    const int cache_row = sq.row;
     const f16 *ks = (const f16 *)a.k_new.ptr + int64_t(b) * a.k_new.batch_stride + int64_t(t) * a.k_new.row_stride +
                     int64_t(hk) * a.k_new.head_stride + 8 * c;
     const f16 *vs = (const f16 *)a.v_new.ptr + int64_t(b) * a.v_new.batch_stride + int64_t(t) * a.v_new.row_stride +
@@ -130,10 +159,12 @@ __global__ __launch_bounds__(256, KvCfg<HD>::NST == 1 ? 2 : 1) void kv_splitkv_k
         const int G = a.nheads / a.nheads_k;
         const int R = G * a.seqlen_q;  // rows of this (batch, kv head): row = qpos * G + g
 
-        const int L = a.cache_seqlens[b] + a.seqlen_new;
+        const KvSeq sq = kv_seq(a, b);
+        if (sq.err && a.status && tid == 0) atomicOr(a.status, sq.err);
+        const int L = sq.err ? 0 : sq.L0 + a.seqlen_new;
         const int S = a.num_splits;
         const int s0 = int((int64_t(L) * split) / S), s1 = int((int64_t(L) * (split + 1)) / S);
-        const int cache_row = a.cache_batch_idx ? a.cache_batch_idx[b] : b;
+        const int cache_row = sq.row;
 
         // This lane's query row.
         const int row = rt * 32 + col;

@@ -321,8 +321,12 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
                                         std::optional<at::Tensor> alibi_slopes, std::optional<at::Tensor> out_opt,
                                         const float softmax_scale, bool is_causal, int window_size_left,
                                         int window_size_right, const float softcap, bool rotary_interleaved,
-                                        int num_splits) {
-    // Order and texts follow flash_api.cpp:530-628.
+                                        int num_splits, std::optional<at::Tensor> status_opt) {
+    // Order and texts follow flash_api.cpp:530-628.  status (optional, after
+    // the reference's arguments): an int32 device word; when given, the cache
+    // capacity and cache_batch_idx bounds are checked on the device instead of
+    // by host reads (no synchronisation, so the call can be graph-captured):
+    // 1 (capacity) / 2 (cache row) are ORed into it for the caller to report.
     (void)rotary_interleaved;
     TORCH_CHECK(!rotary_cos.has_value() && !rotary_sin.has_value(),
                 "Turing KV-cache does not support rotary embeddings yet");
@@ -371,6 +375,7 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
         seqlen_cache = block_table.size(1) * page_block_size;
         batch_size_cache = batch_size;
     }
+    TORCH_CHECK(seqlen_cache <= INT32_MAX, "KV cache capacity must be below 2^31 tokens per sequence");
 
     at::Tensor cache_batch_idx;
     const bool has_cache_batch_idx = cache_batch_idx_opt.has_value();
@@ -406,12 +411,21 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     }
 
     c10::DeviceGuard guard(q.device());
-    // Host-visible checks keep the reference's semantics (two device-to-host reads).
-    if (batch_size > 0) {
+    int32_t *status = nullptr;
+    if (status_opt.has_value()) {
+        const at::Tensor &st = *status_opt;
+        TORCH_CHECK(st.is_cuda() && st.device() == q.device() && st.scalar_type() == at::kInt && st.numel() >= 1 &&
+                        st.is_contiguous(),
+                    "status must be a contiguous int32 tensor on the device of q");
+        status = st.data_ptr<int32_t>();
+    }
+    // Without a status word, the reference's host-visible checks (two
+    // device-to-host reads); the kernels bound every access either way.
+    if (!status && batch_size > 0) {
         const int64_t max_end = cache_seqlens.max().item<int>() + seqlen_new;
         TORCH_CHECK(max_end <= seqlen_cache, "cache capacity is insufficient for the requested append length");
     }
-    if (has_cache_batch_idx && batch_size > 0) {
+    if (!status && has_cache_batch_idx && batch_size > 0) {
         at::Tensor idx_cpu = cache_batch_idx.to(at::kCPU);
         const int32_t *p = idx_cpu.data_ptr<int32_t>();
         for (int64_t i = 0; i < batch_size; ++i)
@@ -457,6 +471,9 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
     a.num_splits = 1;
+    a.cache_capacity = int32_t(seqlen_cache);
+    a.cache_batch = has_block_table ? 0 : int32_t(batch_size_cache);
+    a.status = status;
 
     check_rc(fa_kv_append(&a, stream), "fa_kv_append");
 
@@ -501,6 +518,8 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     f.lse_seqlen = int32_t(seqlen_q);
     f.softmax_scale = softmax_scale;
     f.causal = is_causal ? 1 : 0;
+    f.k_batch = int32_t(batch_size_cache);
+    f.status = status;
     check_rc(fa_fwd(&f, stream), "fa_fwd (kv-cache chunk)");
     return {out, lse};
 }
@@ -517,5 +536,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("out"), py::arg("l"), py::arg("dout"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_k"),
           py::arg("max_seqlen_q"), py::arg("max_seqlen_k"), py::arg("softmax_scale"), py::arg("is_causal"),
           py::arg("dq") = py::none(), py::arg("dk") = py::none(), py::arg("dv") = py::none());
-    m.def("fwd_kvcache", &mha_fwd_kvcache, "KV-cache forward pass");
+    m.def("fwd_kvcache", &mha_fwd_kvcache, "KV-cache forward pass", py::arg("q"), py::arg("k_cache"),
+          py::arg("v_cache"), py::arg("k"), py::arg("v"), py::arg("cache_seqlens"), py::arg("rotary_cos"),
+          py::arg("rotary_sin"), py::arg("cache_batch_idx"), py::arg("cache_leftpad"), py::arg("block_table"),
+          py::arg("alibi_slopes"), py::arg("out"), py::arg("softmax_scale"), py::arg("is_causal"),
+          py::arg("window_size_left"), py::arg("window_size_right"), py::arg("softcap"),
+          py::arg("rotary_interleaved"), py::arg("num_splits"), py::arg("status") = py::none());
 }

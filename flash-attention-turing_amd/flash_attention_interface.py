@@ -89,7 +89,7 @@ def _flash_attn_varlen_backward(
 
 def _flash_attn_kvcache_forward(
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale: float, causal: bool,
-    num_splits: int,
+    num_splits: int, status: Optional[torch.Tensor] = None,
 ):
     tensors = (q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table)
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table = (maybe_contiguous(t) for t in tensors)
@@ -107,6 +107,7 @@ def _flash_attn_kvcache_forward(
         0.0,                   # softcap
         True,                  # rotary_interleaved
         num_splits,
+        status,                # device-side input checks instead of host reads, when given
     )
     return out, lse
 
@@ -344,6 +345,56 @@ def _cache_capacity(k_cache: torch.Tensor, block_table: Optional[torch.Tensor]) 
     return k_cache.shape[1] if block_table is None else block_table.shape[1] * k_cache.shape[1]
 
 
+# Status words of the synchronisation-free KV-cache mode, one int32 per device.
+_KV_STATUS = {}
+
+# Bits of a status word and the errors the synchronous checks raise for them
+# (interface.py:855-857 for the capacity, flash_api.cpp:634-641 for the rows).
+_KV_STATUS_ERRORS = (
+    (1, ValueError, "cache capacity is insufficient for the requested append length"),
+    (2, RuntimeError, "cache_batch_idx entries must be within cache batch bounds"),
+)
+
+
+def _kv_status(device: torch.device) -> torch.Tensor:
+    index = torch.device(device).index
+    if index is None:
+        index = torch.cuda.current_device()
+    st = _KV_STATUS.get(index)
+    if st is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "flash_attn_with_kvcache(validate=False) needs its status word allocated before graph capture: "
+                "call flash_attn_kvcache_check() once on this device first"
+            )
+        st = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", index))
+        _KV_STATUS[index] = st
+    return st
+
+
+def flash_attn_kvcache_check(device: Optional[Union[torch.device, int]] = None) -> None:
+    """Report what earlier flash_attn_with_kvcache(validate=False) calls on a
+    device found wrong, then clear it.
+
+    Such calls read neither cache_seqlens nor cache_batch_idx on the host; the
+    kernels check them instead.  A sequence that would overflow its cache, or
+    whose cache_batch_idx is outside the cache, is left unchanged in the cache
+    and gets O = 0 (LSE 0); this function then raises the error the default
+    (validate=True) call raises at once: ValueError for the capacity,
+    RuntimeError for the cache row.  It reads the device (a synchronisation),
+    so call it outside captured graphs, for instance after each replay or
+    every few steps.  It also allocates the device's status word, which must
+    exist before a validate=False call is captured.
+    """
+    st = _kv_status(torch.device("cuda", device) if isinstance(device, int) else (device or torch.device("cuda")))
+    bits = int(st.item())
+    if bits:
+        st.zero_()
+        for bit, exc, msg in _KV_STATUS_ERRORS:
+            if bits & bit:
+                raise exc(msg)
+
+
 def flash_attn_with_kvcache(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -364,6 +415,7 @@ def flash_attn_with_kvcache(
     alibi_slopes: Optional[torch.Tensor] = None,
     num_splits: int = 0,
     return_softmax_lse: bool = False,
+    validate: bool = True,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """KV-cache attention for inference (signature of upstream FlashAttention).
 
@@ -371,6 +423,13 @@ def flash_attn_with_kvcache(
     caches via block_table, in-place append of k/v at cache_seqlens and split-KV
     (num_splits, 0 = heuristic).  Rotary, ALiBi, local windows, softcap and
     cache_leftpad raise NotImplementedError, as in the reference.
+
+    validate (after the reference's arguments): True checks the cache capacity
+    and cache_batch_idx on the host, raising at once as the reference does (two
+    device reads, so no graph capture).  False skips those reads: the kernels
+    check every sequence themselves (an out-of-range one is neither appended to
+    nor attended over) and record the error for flash_attn_kvcache_check(),
+    so a decode step can be captured in a HIP graph.
     """
     # Validation order of interface.py:807-867.
     _validate_unsupported_kvcache_args(rotary_cos, rotary_sin, cache_leftpad, window_size, softcap, alibi_slopes)
@@ -419,9 +478,10 @@ def flash_attn_with_kvcache(
         if k.shape[1] != v.shape[1]:
             raise ValueError("k and v sequence length must match")
         seqlen_new = k.shape[1]
-    max_cache_usage = int(cache_seqlens.max().item()) if cache_seqlens.numel() > 0 else 0
-    if max_cache_usage + seqlen_new > _cache_capacity(k_cache, block_table):
-        raise ValueError("cache capacity is insufficient for the requested append length")
+    if validate:
+        max_cache_usage = int(cache_seqlens.max().item()) if cache_seqlens.numel() > 0 else 0
+        if max_cache_usage + seqlen_new > _cache_capacity(k_cache, block_table):
+            raise ValueError("cache capacity is insufficient for the requested append length")
     if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda):
         raise RuntimeError("q, k_cache, v_cache must be CUDA tensors")
     if q.dtype != torch.float16 or k_cache.dtype != torch.float16 or v_cache.dtype != torch.float16:
@@ -433,7 +493,9 @@ def flash_attn_with_kvcache(
             raise RuntimeError("k and v must be float16 tensors")
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** (-0.5)
+    status = None if validate else _kv_status(q.device)
     out, lse = _flash_attn_kvcache_forward(
-        q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale, causal, num_splits
+        q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale, causal, num_splits,
+        status,
     )
     return (out, lse) if return_softmax_lse else out

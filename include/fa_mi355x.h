@@ -61,6 +61,13 @@ typedef struct fa_fwd_args {
     int32_t lse_seqlen;             /* seqlen_q, or max_seqlen_q for varlen      */
     float softmax_scale;
     int32_t causal;                 /* bottom-right aligned (mask.h:52)          */
+    /* KV-cache chunk checks, done on the device (no host read; replaces the
+     * reference's host-side checks flash_api.cpp:627, 634-641): with seqused_k,
+     * a batch whose key count is negative or above seqlen_k, or whose
+     * k_batch_idx is outside [0, k_batch), is given no keys (O = 0, LSE = 0)
+     * and, when status is set, ORs 1 (capacity) or 2 (cache row) into *status. */
+    int32_t k_batch;                /* batches of k/v bounding k_batch_idx, 0 = unchecked */
+    int32_t *status;                /* device int32 error word, or NULL          */
 } fa_fwd_args;
 
 int fa_fwd(const fa_fwd_args *args, void *stream);
@@ -123,6 +130,15 @@ typedef struct fa_kvcache_args {
     int32_t *batch_order;           /* workspace [batch + 1]: sequences longest first and a work
                                        counter (both filled by fa_kv_splitkv), or NULL for the
                                        natural order                                           */
+    /* Device-side input checks (replace the host reads of flash_api.cpp:627,
+     * 634-641 and interface.py:855, so a decode step needs no host sync): a
+     * sequence with cache_seqlens[b] < 0, cache_seqlens[b] + seqlen_new >
+     * cache_capacity, or cache_batch_idx[b] outside [0, cache_batch) is not
+     * appended to and is attended over no keys (O = 0, LSE = 0); with status
+     * set, 1 (capacity) or 2 (cache row) is ORed into *status.  0 = unchecked. */
+    int32_t cache_capacity;         /* tokens one sequence's cache holds (paged: pages * page size) */
+    int32_t cache_batch;            /* rows of a contiguous cache (bounds cache_batch_idx)         */
+    int32_t *status;                /* device int32 error word, or NULL                            */
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);

@@ -138,8 +138,11 @@ def test_public_signatures_match_reference():
     assert names == [
         "q", "k_cache", "v_cache", "k", "v", "rotary_cos", "rotary_sin", "cache_seqlens", "cache_batch_idx",
         "cache_leftpad", "block_table", "softmax_scale", "causal", "window_size", "softcap", "rotary_interleaved",
-        "alibi_slopes", "num_splits", "return_softmax_lse",
+        "alibi_slopes", "num_splits", "return_softmax_lse", "validate",
     ]
+    # The reference's parameters, in order, then one of this build's: validate
+    # (keyword, default True = the reference's host-side checks).
+    assert sig.parameters["validate"].default is True
     assert sig.parameters["num_splits"].default == 0 and sig.parameters["window_size"].default == (-1, -1)
     assert list(inspect.signature(fai.flash_attn_func).parameters) == ["q", "k", "v", "softmax_scale", "causal"]
     assert list(inspect.signature(fai.flash_attn_varlen_func).parameters) == [
@@ -187,3 +190,24 @@ def test_packed_inputs_are_views():
     g, (a, b) = fai._packed_grad((torch.Size([7, 2, 3, 64]), torch.float16, torch.device("cpu")), 1, True)
     assert g.shape == (7, 2, 3, 64) and not g.any()
     assert a.data_ptr() == g[:, 0].data_ptr() and b.data_ptr() == g[:, 1].data_ptr()
+
+
+def test_kvcache_status_errors_match_sync_checks():
+    # The status bits of the synchronisation-free mode map to the exceptions and
+    # texts of the synchronous checks (capacity: ValueError, as pinned by
+    # test_flash_attn.py:2084-2093; cache row: the extension's RuntimeError).
+    errs = dict((bit, (exc, msg)) for bit, exc, msg in fai._KV_STATUS_ERRORS)
+    assert errs[1] == (ValueError, "cache capacity is insufficient for the requested append length")
+    assert errs[2] == (RuntimeError, "cache_batch_idx entries must be within cache batch bounds")
+    assert callable(fai.flash_attn_kvcache_check)
+
+
+def test_kvcache_validate_false_skips_host_capacity_read():
+    # With validate=False the capacity is not checked on the host: a CPU call
+    # that would fail the capacity check reaches the device check instead.
+    q, kc = _t(1, 1, 2, 64, dtype=torch.float16), _t(1, 8, 2, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="cache capacity is insufficient"):
+        fai.flash_attn_with_kvcache(q, kc, kc.clone(), cache_seqlens=torch.full((1,), 9, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="must be CUDA tensors"):
+        fai.flash_attn_with_kvcache(q, kc, kc.clone(), cache_seqlens=torch.full((1,), 9, dtype=torch.int32),
+                                    validate=False)
