@@ -455,16 +455,21 @@ extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
 extern "C" int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seqlen_q, int batch,
                                 int nheads, int nheads_k, int num_cus) {
     // An explicit request is honoured (kvcache_native.cu:922-924).  Otherwise
-    // split only when the (batch, kv head, row tile) workgroups cannot fill
-    // two rounds of the chip, and keep at least 512 keys per split.
+    // (measured on MI355X over paged and contiguous decode shapes) a work item
+    // streams best with about 8192 cache positions: fewer and the per-item
+    // start-up and the combine weigh in, more and the longest-first deal
+    // balances worse.  Enough splits are also taken for one item per compute
+    // unit, and a split keeps at least 512 positions.  Only the capacity is
+    // known on the host (the live lengths are on the device).
     (void)head_dim;
     if (requested > 0) return requested;
-    if (batch <= 0 || nheads_k <= 0 || nheads <= 0) return 1;
+    if (batch <= 0 || nheads_k <= 0 || nheads <= 0 || seqlen_k_capacity <= 0) return 1;
     const int rows = (nheads / nheads_k) * seqlen_q;
     const int64_t wgs = int64_t(batch) * nheads_k * ((rows + 31) / 32);
-    const int max_by_len = std::max(1, seqlen_k_capacity / 512);
-    const int64_t want = (2 * int64_t(std::max(num_cus, 1)) + wgs - 1) / std::max<int64_t>(wgs, 1);
-    return int(std::max<int64_t>(1, std::min<int64_t>({want, int64_t(max_by_len), 128})));
+    const int64_t by_len = (int64_t(seqlen_k_capacity) + 4096) / 8192;
+    const int64_t by_fill = (int64_t(std::max(num_cus, 1)) + wgs - 1) / std::max<int64_t>(wgs, 1);
+    const int64_t max_by_len = std::max(1, seqlen_k_capacity / 512);
+    return int(std::max<int64_t>(1, std::min<int64_t>({std::max(by_len, by_fill), max_by_len, 128})));
 }
 
 extern "C" size_t fa_kv_workspace_bytes(const fa_kvcache_args *a) {

@@ -55,6 +55,18 @@ def test_num_splits_heuristic(lib):
     s = f(0, 32768, 128, 1, 4, 32, 8, 256)
     assert 1 < s <= 64
     assert f(0, 1 << 20, 128, 1, 1, 8, 1, 256) <= 128
+    # The split counts measured best on MI355X (256 CUs) for these decode shapes:
+    # (capacity, head_dim, seqlen_q, batch, heads, kv heads) -> splits
+    measured_best = {
+        (32768 + 256, 128, 1, 64, 32, 8): 4,   # c4: paged, lengths 1k-32k
+        (32768 + 256, 128, 1, 8, 32, 8): 4,    # 8 x 32k
+        (131072 + 256, 128, 1, 1, 32, 8): 32,  # 1 x 128k
+        (131072, 64, 4, 4, 16, 16): 16,        # c5: 4 query tokens, 65k-131k
+        (8192, 128, 1, 16, 32, 8): 2,          # 16 x 8k
+    }
+    for (cap, d, sq, b, h, hk), best in measured_best.items():
+        assert f(0, cap, d, sq, b, h, hk, 256) == best
+    assert f(0, 4096, 128, 1, 256, 32, 8, 256) == 1  # large batches fill the chip unsplit
 
 
 def test_ctypes_structs_match_the_c_layout(tmp_path):
