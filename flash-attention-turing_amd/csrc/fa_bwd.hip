@@ -293,6 +293,11 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     load_rows(ks_lds, kp, a.k.row_stride);
     load_rows(vs_lds, vp, a.v.row_stride);
     wait_vmem();  // only the tile copies are in flight inside the loop
+    __syncthreads();
+    // The wave's K rows stay in registers as the S B operands for the whole kernel.
+    f16x8 kreg[HD / 16];
+#pragma unroll
+    for (int g = 0; g < HD / 16; ++g) kreg[g] = rd0.a_operand(ks_lds, 32 * kg, g);
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) {
@@ -368,10 +373,9 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
         // accumulators, the S/dP tiles and the operands in flight fit the
         // 256 registers of a two-waves-per-SIMD wave.
         constexpr int PIPE = 2, NG = HD / 16;
-        f16x8 qa[PIPE], ka[PIPE], oa[PIPE], va[PIPE];
+        f16x8 qa[PIPE], oa[PIPE], va[PIPE];
         auto ld = [&](int g) {
             qa[g % PIPE] = rd.a_operand(qt, r0, g);
-            ka[g % PIPE] = rd.a_operand(ks_lds, 32 * kg, g);
             oa[g % PIPE] = rd.a_operand(ot, r0, g);
             va[g % PIPE] = rd.a_operand(vs_lds, 32 * kg, g);
         };
@@ -395,7 +399,7 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             if (g + PIPE - 1 < NG) ld(g + PIPE - 1);
-            s = mfma32(qa[g % PIPE], ka[g % PIPE], s);
+            s = mfma32(qa[g % PIPE], kreg[g], s);
             dp = mfma32(oa[g % PIPE], va[g % PIPE], dp);
             __builtin_amdgcn_sched_barrier(0);
         }
