@@ -393,33 +393,79 @@ __global__ __launch_bounds__(256) void kv_order_kernel(const fa_kvcache_args a) 
 }
 
 // ---------------------------------------------------------------------------
-// Combine: one wave per (batch, head, qpos) row.
+// Combine: one wave per (batch, head, qpos) row.  Lane s reads split s's LSE
+// (further rounds past 64 splits) while the partial outputs of the first
+// kPreSplits splits are loaded at the same time; the maximum and the weight
+// sum are wave reductions, and each lane sums HD / 64 output elements over
+// the splits with the weight exp(lse_s - lse_total) taken from lane s.
+constexpr int kPreSplits = 16;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void kv_combine_kernel(const fa_kvcache_args a) {
+    constexpr int DPL = HD / 64;  // output elements per lane
+    typedef float fdpl __attribute__((ext_vector_type(DPL)));
     const int nrow = a.batch * a.nheads * a.seqlen_q;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= nrow) return;
     const int S = a.num_splits;
-    float lmax = -INFINITY;
-    for (int s = 0; s < S; ++s) lmax = fmaxf(lmax, a.lse_accum[int64_t(s) * nrow + r]);
-    float wsum = 0.f;
-    if (lmax != -INFINITY)
-        for (int s = 0; s < S; ++s) wsum += expf(a.lse_accum[int64_t(s) * nrow + r] - lmax);
+    auto part_ptr = [&](int s) {
+        return reinterpret_cast<const fdpl *>(a.out_accum + (int64_t(s) * nrow + r) * HD + DPL * lane);
+    };
+    // Splits past S re-read split S - 1 (finite) and get weight 0 below.
+    fdpl pre[kPreSplits];
+#pragma unroll
+    for (int s = 0; s < kPreSplits; ++s) pre[s] = *part_ptr(min(s, S - 1));
+    const float lse0 = lane < S ? a.lse_accum[int64_t(lane) * nrow + r] : -INFINITY;
+    float lmax = lse0;
+    for (int s0 = 64; s0 < S; s0 += 64)
+        if (s0 + lane < S) lmax = fmaxf(lmax, a.lse_accum[int64_t(s0 + lane) * nrow + r]);
+    lmax = wave_max(lmax);
+    float part = 0.f;
+    if (lmax != -INFINITY) {
+        if (lane < S) part = expf(lse0 - lmax);
+        for (int s0 = 64; s0 < S; s0 += 64)
+            if (s0 + lane < S) part += expf(a.lse_accum[int64_t(s0 + lane) * nrow + r] - lmax);
+    }
+    const float wsum = wave_sum(part);
     const bool live = lmax != -INFINITY && wsum > 0.f;
     const float ltot = live ? lmax + logf(wsum) : -INFINITY;
+    fdpl acc;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+    if (live) {
+        const float w0 = lane < S ? expf(lse0 - ltot) : 0.f;
+        auto weight = [](float w, int s) {
+            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+        };
+#pragma unroll
+        for (int s = 0; s < kPreSplits; ++s) acc += weight(w0, s) * pre[s];  // lane s >= S holds w0 = 0
+        for (int s0 = 0; s0 < S; s0 += 64) {
+            const float w = s0 == 0 ? w0
+                                    : (s0 + lane < S ? expf(a.lse_accum[int64_t(s0 + lane) * nrow + r] - ltot) : 0.f);
+            const int n = min(64, S - s0);
+#pragma unroll 1
+            for (int s = s0 == 0 ? kPreSplits : 0; s < n; ++s) acc += weight(w, s) * *part_ptr(s0 + s);
+        }
+    }
     const int qp = r % a.seqlen_q;
     const int bh = r / a.seqlen_q;
     const int h = bh % a.nheads, b = bh / a.nheads;
     f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
-              int64_t(h) * a.o.head_stride;
-    for (int d = lane; d < HD; d += 64) {
-        float acc = 0.f;
-        if (live)
-            for (int s = 0; s < S; ++s)
-                acc += expf(a.lse_accum[int64_t(s) * nrow + r] - ltot) * a.out_accum[(int64_t(s) * nrow + r) * HD + d];
-        op[d] = (f16)acc;
-    }
+              int64_t(h) * a.o.head_stride + DPL * lane;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) op[i] = (f16)acc[i];
     if (lane == 0) a.lse[r] = live ? ltot : 0.f;
 }
 

@@ -125,7 +125,7 @@ typedef struct fa_kvcache_args {
     int32_t num_splits;             /* >= 1, as resolved by fa_kv_num_splits     */
     float softmax_scale;
     int32_t causal;
-    float *out_accum;               /* workspace [num_splits][batch*nheads*seqlen_q][d] fp32 */
+    float *out_accum;               /* workspace [num_splits][batch*nheads*seqlen_q][d] fp32, 8-byte aligned */
     float *lse_accum;               /* workspace [num_splits][batch*nheads*seqlen_q] fp32    */
     int32_t *batch_order;           /* workspace [batch + 1]: sequences longest first and a work
                                        counter (both filled by fa_kv_splitkv), or NULL for the
