@@ -118,11 +118,12 @@ struct KvCfg {
     static constexpr int KCH = HD / 8;
     static constexpr int TILE = kTile * HD * 2;         // one K or V tile, natural layout
     static constexpr int STAGE = 2 * TILE;              // K tile, then V tile
-    // Ring stages per wave.  One stage suffices: a tile's operands are read
-    // into registers and the stage is refilled before the tile is computed,
-    // and the smaller footprint lets two workgroups share a CU (one's start-up
-    // and merge overlap the other's streaming).
-    static constexpr int NST = 1;
+    // Ring stages per wave.  A tile's operands are read into registers and the
+    // stage is refilled before the tile is computed, so one stage keeps a tile
+    // in flight; at head_dim 64 a second stage (more bytes in flight, +1 % on a
+    // long-context decode) still lets two workgroups share a CU, at 128 it
+    // would not (one's start-up and merge overlap the other's streaming).
+    static constexpr int NST = HD == 64 ? 2 : 1;
     static constexpr int WAVE_LDS = NST * STAGE;        // also holds HD x 32 fp32 at the merge
     static constexpr int CPW = kTile * KCH / 64;        // copies per lane per tile (K or V)
     static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
@@ -136,7 +137,7 @@ struct KvCfg {
 // the items are dealt out greedily in that order.  The counter
 // (batch_order[batch]) is zeroed by kv_order_kernel on the same stream.
 template <int HD, bool DYN>
-__global__ __launch_bounds__(256, KvCfg<HD>::NST == 1 ? 2 : 1) void kv_splitkv_kernel(const fa_kvcache_args a,
+__global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a,
                                                                                    const int row_tiles,
                                                                                    const int n_items) {
     using C = KvCfg<HD>;
