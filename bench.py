@@ -46,10 +46,10 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 # (FETCH x 2.0, WRITE x 1.0); summary in profiles/hbm_bytes_pmc_c2_c4.md.
 # Re-measured whenever a kernel changes; None where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 8.386e8 + 6.819e7,
-    "bwd_dq": 6.799e8 + 7.355e7,
-    "bwd_dkdv": 7.254e8 + 1.450e8,
-    "kv_splitkv": 4.697e9 + 8.658e6,
+    "fwd": 6.609e8 + 6.816e7,
+    "bwd_dq": 6.007e8 + 7.353e7,
+    "bwd_dkdv": 7.438e8 + 1.512e8,
+    "kv_splitkv": 4.696e9 + 8.657e6,
 }
 
 
