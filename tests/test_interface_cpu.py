@@ -211,3 +211,32 @@ def test_kvcache_validate_false_skips_host_capacity_read():
     with pytest.raises(RuntimeError, match="must be CUDA tensors"):
         fai.flash_attn_with_kvcache(q, kc, kc.clone(), cache_seqlens=torch.full((1,), 9, dtype=torch.int32),
                                     validate=False)
+
+
+def test_no_fallback_without_the_native_library(tmp_path):
+    # The product path is the native library or an error: the interface cannot
+    # be imported without the extension, and the C-ABI loader refuses a
+    # missing library (no CPU math path behind either).
+    import subprocess
+    import sys
+
+    import fa_capi
+
+    code = (
+        "import sys; sys.modules['flash_attn_turing'] = None\n"
+        "try:\n"
+        "    import flash_attention_interface\n"
+        "except ImportError:\n"
+        "    print('raised')\n"
+    )
+    env_path = ":".join(sys.path)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                       env={"PYTHONPATH": env_path, "PATH": "/usr/bin:/bin"}, timeout=300)
+    assert r.stdout.strip() == "raised", r.stdout + r.stderr
+    saved = fa_capi._lib
+    try:
+        fa_capi._lib = None
+        with pytest.raises(ImportError, match="is not built"):
+            fa_capi.load(str(tmp_path / "libfa_mi355x.so"))
+    finally:
+        fa_capi._lib = saved
