@@ -97,3 +97,63 @@ def test_ctypes_structs_match_the_c_layout(tmp_path):
         st = structs[cname]
         expect = ctypes.sizeof(st) if field == "size" else getattr(st, field).offset
         assert int(value) == expect, f"{cname}.{field}: C {value} vs ctypes {expect}"
+
+
+def _capi():
+    import sys
+
+    sys.path.insert(0, os.path.join(REPO, "flash-attention-turing_amd"))
+    import fa_capi
+
+    return fa_capi
+
+
+def test_validation_errors_before_any_launch(lib):
+    # Each entry point checks its arguments before touching the device, so
+    # these calls return codes on a machine without a GPU.  Pointers are fake
+    # but 16-byte aligned; nothing is dereferenced.
+    fa_capi = _capi()
+    T = fa_capi.FaTensor
+    P = 1 << 20  # an aligned fake device address
+
+    def tensor(ptr=P, rs=1024, hs=128):
+        return T(ptr, 0, rs, hs)
+
+    f = fa_capi.FaFwdArgs()
+    f.q = f.k = f.v = f.o = tensor()
+    f.lse = P
+    f.batch, f.seqlen_q, f.seqlen_k, f.nheads, f.nheads_k, f.head_dim, f.lse_seqlen = 1, 8, 8, 4, 2, 96, 8
+    fwd = lib.fa_fwd
+    fwd.argtypes = [ctypes.POINTER(fa_capi.FaFwdArgs), ctypes.c_void_p]
+    assert fwd(ctypes.byref(f), None) == -2  # head_dim 96: unsupported
+    f.head_dim, f.nheads_k = 128, 3
+    assert fwd(ctypes.byref(f), None) == -1  # 4 q-heads over 3 kv heads
+    f.nheads_k, f.lse_seqlen = 2, 4
+    assert fwd(ctypes.byref(f), None) == -1  # LSE rows shorter than seqlen_q
+    f.lse_seqlen = 8
+    f.q = tensor(P + 8)
+    assert fwd(ctypes.byref(f), None) == -1  # q not 16-byte aligned
+    f.q = tensor(rs=1020)
+    assert fwd(ctypes.byref(f), None) == -1  # row stride not a multiple of 8 elements
+
+    kv = fa_capi.FaKvcacheArgs()
+    kv.q = kv.k_cache = kv.v_cache = kv.o = tensor()
+    kv.lse = kv.cache_seqlens = P
+    kv.batch, kv.seqlen_q, kv.nheads, kv.nheads_k, kv.head_dim = 2, 1, 4, 2, 128
+    kv.num_splits = 4  # needs the split accumulators
+    split = lib.fa_kv_splitkv
+    split.argtypes = [ctypes.POINTER(fa_capi.FaKvcacheArgs), ctypes.c_void_p]
+    assert split(ctypes.byref(kv), None) == -3
+    kv.num_splits = 0
+    assert split(ctypes.byref(kv), None) == -1  # num_splits must be >= 1 here
+    kv.num_splits, kv.block_table, kv.page_block_size = 1, P, 100
+    assert split(ctypes.byref(kv), None) == -1  # page size not a multiple of the 32-key tile
+    kv.page_block_size, kv.cache_batch_idx = 256, P
+    assert split(ctypes.byref(kv), None) == -1  # paged and remapped at once
+    ws = lib.fa_kv_workspace_bytes
+    ws.argtypes = [ctypes.POINTER(fa_capi.FaKvcacheArgs)]
+    ws.restype = ctypes.c_size_t
+    kv.num_splits = 3
+    assert ws(ctypes.byref(kv)) == 3 * 2 * 4 * 1 * (128 + 1) * 4
+    kv.num_splits = 1
+    assert ws(ctypes.byref(kv)) == 0
