@@ -14,7 +14,9 @@ inputs already resident in HBM:
   point the 50 % / 35 % MFMA targets are quoted on), the packed varlen GQA
   step (config c3, seed 2), the paged split-KV decode with append (config c4,
   seed 3) and the long-context remapped-cache decode (config c5, seed 4), the
-  last two in HBM GB/s.  ``--no-8k`` keeps only the headline shapes (c2, c4).
+  last two in HBM GB/s, and c4 again with a 4096-key sliding window
+  (``decode_c4_window4k``: an upstream option the reference rejects).
+  ``--no-8k`` keeps only the headline shapes (c2, c4).
 
 Per-kernel durations come from HIP events recorded on the launch stream
 between the launches of the timed region.  The CPU baseline is PyTorch's CPU
@@ -147,8 +149,10 @@ def train_report(batch, seqlen, heads, hd, ms_step, per):
     }, flops, unit
 
 
-def decode_setup(device, seed=3):
-    """Config c4: paged decode with append, b64, 32 q / 8 kv heads, d128, page 256, splits 8."""
+def decode_setup(device, seed=3, window=None):
+    """Config c4: paged decode with append, b64, 32 q / 8 kv heads, d128, page 256, splits 8.
+    ``window`` (left, right): the same call with a local window; the byte counts
+    then cover the keys inside it."""
     import torch
 
     import fa_capi
@@ -182,13 +186,16 @@ def decode_setup(device, seed=3):
     order = torch.empty(b + 1, dtype=torch.int32, device=device)  # ranks + work counter
     args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, seqlens, d ** -0.5, True, splits, k_new=k_new,
                                 v_new=v_new, block_table=table_d, out_accum=ws[: splits * rows * d],
-                                lse_accum=ws[splits * rows * d :], batch_order=order)
+                                lse_accum=ws[splits * rows * d :], batch_order=order,
+                                window=window or (-1, -1))
     launches = [
         ("kv_append", lambda: fa_capi.call("fa_kv_append", args)),
         ("kv_splitkv", lambda: fa_capi.call("fa_kv_splitkv", args)),
         ("kv_combine", lambda: fa_capi.call("fa_kv_combine", args)),
     ]
     ends = lens + 1
+    if window is not None and window[0] >= 0:
+        ends = torch.clamp(ends, max=window[0] + 1)  # keys inside the window of the one query
     kv_bytes = int(ends.sum()) * hk * d * 2 * 2
     other = (2 * b * h * d * 2  # q read, out write
              + 2 * 2 * b * hk * d * 2  # k/v new read + write
@@ -423,6 +430,22 @@ def main():
         log(f"decode: {info}")
         del launches, outs
         torch.cuda.empty_cache()
+        if not args.no_8k:
+            # The same decode with a 4096-key sliding window (an upstream option the
+            # reference rejects): the kernel skips the tiles outside the window.
+            log("decode c4 with window_size (4095, -1)")
+            launchesw, infow, outsw = decode_setup(device, window=(4095, -1))
+            msw, perw = Timed(launchesw).run(args.steps, args.warmup)
+            assert torch.isfinite(outsw["out"]).all(), "non-finite windowed decode output"
+            tw = sum(perw.values())
+            result["decode_c4_window4k"] = dict(
+                window=[4095, -1], kv_bytes_in_window=infow["kv_bytes"], ms_per_call=round(msw, 4),
+                kernels_ms={k: round(v, 4) for k, v in perw.items()},
+                gbs_call=round(infow["bytes"] / (tw * 1e-3) / 1e9, 1),
+                speedup_vs_full_cache=round(info["ms_per_call"] / msw, 2))
+            log(f"decode window: {result['decode_c4_window4k']}")
+            del launchesw, outsw
+            torch.cuda.empty_cache()
         if not args.no_8k:
             log("long-context c5: contiguous 8 x 131072 cache, remapped rows, 4-token append, 16 splits (seed 4)")
             launches5, info5, outs5 = longctx_setup(device)

@@ -129,6 +129,13 @@ struct KvCfg {
     static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
 };
 
+// tanh x = 1 - 2 / (e^(2x) + 1): exactly +-1 at the ends, an absolute error of a
+// few fp32 ulps of 1 in between (what a softcapped score needs).
+__device__ __forceinline__ float tanh_fast(float x) {
+    const float e = exp2_fast(x * (2.f * kLog2e));
+    return 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+}
+
 // Work items are (sequence rank, split, kv head, row tile), rank slowest: with
 // batch_order the longest sequences' items come first (longest-job-first keeps
 // the last items short).  With DYN the grid is resident (two workgroups per
@@ -136,7 +143,9 @@ struct KvCfg {
 // unclaimed item from a device counter, so no workgroup is relaunched and
 // the items are dealt out greedily in that order.  The counter
 // (batch_order[batch]) is zeroed by kv_order_kernel on the same stream.
-template <int HD, bool DYN>
+// EXT switches on the local window and softcap options (a separate instance,
+// so the plain kernel carries none of their work).
+template <int HD, bool DYN, bool EXT>
 __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a,
                                                                                    const int row_tiles,
                                                                                    const int n_items) {
@@ -172,10 +181,31 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         const bool row_ok = row < R;
         const int qpos = row_ok ? row / G : 0;
         const int hq = hk * G + (row_ok ? row % G : 0);
-        const int lim = a.causal ? qpos + L - a.seqlen_q : L - 1;  // last visible key
+        int lim = a.causal ? qpos + L - a.seqlen_q : L - 1;  // last visible key
+        int w_lo = 0;                                          // first visible key
+        // Keys whose tiles this item walks: the split, narrowed to the union of
+        // its rows' windows.
+        int k_lo = s0, k_hi = s1;
+        if constexpr (EXT) {
+            if (a.local_window) {
+                const int pos = qpos + L - a.seqlen_q;  // the query's own key position
+                if (a.window_right >= 0) lim = min(lim, pos + a.window_right);
+                if (a.window_left >= 0) w_lo = pos - a.window_left;
+                const int p_lo = (rt * 32) / G + L - a.seqlen_q;
+                const int p_hi = (min(R, rt * 32 + 32) - 1) / G + L - a.seqlen_q;
+                int hi = a.causal ? p_hi : L - 1;
+                if (a.window_right >= 0) hi = min(hi, p_hi + a.window_right);
+                if (a.window_left >= 0) k_lo = max(k_lo, p_lo - a.window_left);
+                k_hi = max(k_lo, min(k_hi, hi + 1));
+            }
+        }
 
         const bool neg = a.softmax_scale < 0.f;
-        const float cscale = fabsf(a.softmax_scale) * kLog2e;
+        const bool capped = EXT && a.softcap > 0.f;
+        // The exponent multiplier: scale * log2(e), or log2(e) for softcapped
+        // scores (already scaled); cap_in = scale / softcap.
+        const float cscale = capped ? kLog2e : fabsf(a.softmax_scale) * kLog2e;
+        const float cap_in = capped ? fabsf(a.softmax_scale) / a.softcap : 0.f;
         f16x8 qB[HD / 16];
         {
             const f16 *qp = (const f16 *)a.q.ptr + int64_t(b) * a.q.batch_stride + int64_t(qpos) * a.q.row_stride +
@@ -193,15 +223,15 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
         float m_t = -INFINITY, l_p = 0.f;
 
-        const int t_first = s0 / kTile;
-        const int t_last = s1 > s0 ? (s1 - 1) / kTile : t_first - 1;
+        const int t_first = k_lo / kTile;
+        const int t_last = k_hi > k_lo ? (k_hi - 1) / kTile : t_first - 1;
         const int my_first = t_first + wave;
         const int n_my = my_first <= t_last ? (t_last - my_first) / kKvWaves + 1 : 0;
 
         // Page ids of the split, staged in LDS so the ring never waits on a table read.
         const int page = a.page_block_size;
         const int pg_first = a.block_table ? (t_first * kTile) / page : 0;
-        const int n_pages = a.block_table && s1 > s0 ? (t_last * kTile) / page - pg_first + 1 : 0;
+        const int n_pages = a.block_table && k_hi > k_lo ? (t_last * kTile) / page - pg_first + 1 : 0;
         const bool pages_in_lds = n_pages <= C::MAX_PAGES;
         if (a.block_table && pages_in_lds) {
             const int32_t *bt = a.block_table + int64_t(b) * a.block_table_stride + pg_first;
@@ -270,11 +300,17 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
             f32x16 s = mfma32(ka[0], qB[0], zero16());
     #pragma unroll
             for (int g = 1; g < HD / 16; ++g) s = mfma32(ka[g], qB[g], s);
+            if constexpr (EXT) {
+                if (capped) {
+    #pragma unroll
+                    for (int r = 0; r < 16; ++r) s[r] = a.softcap * tanh_fast(s[r] * cap_in);
+                }
+            }
             float mx = -INFINITY;
     #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = p0 + acc_lrow(r, hh);
-                if (key < s0 || key >= s1 || key > lim) s[r] = -INFINITY;
+                if (key < s0 || key >= s1 || key > lim || (EXT && key < w_lo)) s[r] = -INFINITY;
                 mx = fmaxf(mx, s[r]);
             }
             mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -492,6 +528,7 @@ static int check_kv(const fa_kvcache_args *p) {
         return FA_ERR_INVALID_ARG;
     if (a.block_table && (a.page_block_size <= 0 || a.page_block_size % kTile != 0)) return FA_ERR_INVALID_ARG;
     if (a.block_table && a.cache_batch_idx) return FA_ERR_INVALID_ARG;
+    if (!(a.softcap >= 0.f) || a.softcap == INFINITY) return FA_ERR_INVALID_ARG;  // NaN fails too
     return FA_OK;
 }
 
@@ -572,16 +609,23 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     } else {
         run.batch_order = nullptr;  // natural order
     }
+    const bool ext = a.local_window || a.softcap > 0.f;
+    auto go = [&](auto hd_tag, auto dyn_tag, auto ext_tag) {
+        constexpr int HD = decltype(hd_tag)::value;
+        constexpr bool DYN = decltype(dyn_tag)::value, EXT = decltype(ext_tag)::value;
+        hipLaunchKernelGGL((fa::kv_splitkv_kernel<HD, DYN, EXT>), dim3(grid), dim3(fa::kKvThreads), 0, s, run,
+                           row_tiles, n_items);
+    };
+    using H128 = std::integral_constant<int, 128>;
+    using H64 = std::integral_constant<int, 64>;
+    using T = std::true_type;
+    using F = std::false_type;
     if (a.head_dim == 128) {
-        if (dyn)
-            hipLaunchKernelGGL((fa::kv_splitkv_kernel<128, true>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
-        else
-            hipLaunchKernelGGL((fa::kv_splitkv_kernel<128, false>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
+        if (dyn) ext ? go(H128{}, T{}, T{}) : go(H128{}, T{}, F{});
+        else ext ? go(H128{}, F{}, T{}) : go(H128{}, F{}, F{});
     } else {
-        if (dyn)
-            hipLaunchKernelGGL((fa::kv_splitkv_kernel<64, true>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
-        else
-            hipLaunchKernelGGL((fa::kv_splitkv_kernel<64, false>), dim3(grid), dim3(fa::kKvThreads), 0, s, run, row_tiles, n_items);
+        if (dyn) ext ? go(H64{}, T{}, T{}) : go(H64{}, T{}, F{});
+        else ext ? go(H64{}, F{}, T{}) : go(H64{}, F{}, F{});
     }
     return int(hipGetLastError());
 }

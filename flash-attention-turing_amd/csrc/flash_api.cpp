@@ -23,6 +23,7 @@
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <cmath>
 #include <optional>
 #include <vector>
 
@@ -333,9 +334,9 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     TORCH_CHECK(!cache_leftpad.has_value(), "Turing KV-cache does not support cache_leftpad yet");
     TORCH_CHECK(!alibi_slopes.has_value(), "Turing KV-cache does not support ALiBi yet");
     TORCH_CHECK(!out_opt.has_value(), "Turing KV-cache does not support a preallocated output tensor yet");
-    TORCH_CHECK(window_size_left == -1 && window_size_right == -1,
-                "Turing KV-cache does not support local window attention yet");
-    TORCH_CHECK(softcap == 0.0f, "Turing KV-cache does not support softcap yet");
+    // Local windows and softcap (rejected by the reference, flash_api.cpp:530-539)
+    // take upstream FlashAttention's semantics; they run in the split kernel.
+    TORCH_CHECK(std::isfinite(softcap), "softcap must be finite");
     TORCH_CHECK(num_splits >= 0, "num_splits must be non-negative");
 
     TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda(), "q, k_cache, v_cache must be CUDA tensors");
@@ -474,13 +475,21 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     a.cache_capacity = int32_t(seqlen_cache);
     a.cache_batch = has_block_table ? 0 : int32_t(batch_size_cache);
     a.status = status;
+    // Upstream's normalisation: a bound at least the cache capacity is no bound.
+    if (window_size_left >= seqlen_cache) window_size_left = -1;
+    if (window_size_right >= seqlen_cache) window_size_right = -1;
+    a.local_window = (window_size_left >= 0 || window_size_right >= 0) ? 1 : 0;
+    a.window_left = window_size_left;
+    a.window_right = window_size_right;
+    a.softcap = softcap > 0.f ? softcap : 0.f;
+    const bool options = a.local_window || a.softcap > 0.f;
 
     check_rc(fa_kv_append(&a, stream), "fa_kv_append");
 
     // Routing of flash_api.cpp:668: paged, explicit splits > 1 or single-token decode
     // take the split-KV kernel; a contiguous multi-token chunk takes the tiled
     // forward kernel with per-batch key counts and the batch remap.
-    const bool use_split_kernel = has_block_table || num_splits > 1 || seqlen_q == 1;
+    const bool use_split_kernel = has_block_table || num_splits > 1 || seqlen_q == 1 || options;
     if (use_split_kernel) {
         a.num_splits = fa_kv_num_splits(num_splits, int(seqlen_cache), int(head_size), int(seqlen_q),
                                         int(batch_size), int(num_heads), int(num_heads_k),

@@ -63,6 +63,7 @@ class FaKvcacheArgs(ctypes.Structure):
         ("seqlen_new", _i32), ("page_block_size", _i32), ("num_splits", _i32), ("softmax_scale", _f32),
         ("causal", _i32), ("out_accum", _p), ("lse_accum", _p), ("batch_order", _p),
         ("cache_capacity", _i32), ("cache_batch", _i32), ("status", _p),
+        ("local_window", _i32), ("window_left", _i32), ("window_right", _i32), ("softcap", _f32),
     ]
 
 
@@ -178,7 +179,8 @@ def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, caus
 
 def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: float, causal: bool, num_splits: int,
                  k_new=None, v_new=None, cache_batch_idx=None, block_table=None, out_accum=None,
-                 lse_accum=None, batch_order=None, status=None) -> FaKvcacheArgs:
+                 lse_accum=None, batch_order=None, status=None, window=(-1, -1),
+                 softcap: float = 0.0) -> FaKvcacheArgs:
     a = FaKvcacheArgs()
     a.q, a.k_cache, a.v_cache, a.o = (tensor_desc(x) for x in (q, k_cache, v_cache, o))
     a.k_new, a.v_new = tensor_desc(k_new), tensor_desc(v_new)
@@ -197,4 +199,7 @@ def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: floa
     a.cache_capacity = k_cache.shape[1] * (block_table.shape[1] if block_table is not None else 1)
     a.cache_batch = k_cache.shape[0] if block_table is None else 0
     a.status = ptr(status)
+    a.local_window = int(tuple(window) != (-1, -1))
+    a.window_left, a.window_right = window
+    a.softcap = softcap
     return a

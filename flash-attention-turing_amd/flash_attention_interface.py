@@ -15,6 +15,7 @@ FlashAttnVarlenKVPackedFunc (:172-445).  Every call goes to the native
 math fallback: a missing or incompatible extension raises at import or call.
 """
 
+import math
 from typing import Optional, Tuple, Union
 
 import torch  # noqa: F401  (loads the HIP runtime before the extension)
@@ -89,12 +90,13 @@ def _flash_attn_varlen_backward(
 
 def _flash_attn_kvcache_forward(
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale: float, causal: bool,
-    num_splits: int, status: Optional[torch.Tensor] = None,
+    num_splits: int, status: Optional[torch.Tensor] = None, window_size: Tuple[int, int] = (-1, -1),
+    softcap: float = 0.0,
 ):
     tensors = (q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table)
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table = (maybe_contiguous(t) for t in tensors)
-    # The 20-argument binding of flash_api.cpp:508-528; rotary, leftpad, ALiBi,
-    # a preallocated out, local windows and softcap are passed as "absent".
+    # The 20-argument binding of flash_api.cpp:508-528; rotary, leftpad, ALiBi
+    # and a preallocated out are passed as "absent".
     out, lse = flash_attn_gpu.fwd_kvcache(
         q, k_cache, v_cache, k, v, cache_seqlens,
         None, None,            # rotary_cos, rotary_sin
@@ -103,8 +105,8 @@ def _flash_attn_kvcache_forward(
         block_table,
         None, None,            # alibi_slopes, out
         softmax_scale, causal,
-        -1, -1,                # window_size_left, window_size_right
-        0.0,                   # softcap
+        int(window_size[0]), int(window_size[1]),
+        float(softcap),
         True,                  # rotary_interleaved
         num_splits,
         status,                # device-side input checks instead of host reads, when given
@@ -324,14 +326,16 @@ def flash_attn_varlen_kvpacked_func(
 
 
 def _validate_unsupported_kvcache_args(rotary_cos, rotary_sin, cache_leftpad, window_size, softcap, alibi_slopes):
+    # interface.py:617-634 rejects all five; local windows and softcap are
+    # supported here (upstream FlashAttention's semantics), the rest are not.
     if rotary_cos is not None or rotary_sin is not None:
         raise NotImplementedError("Turing KV-cache does not support rotary embeddings yet")
     if cache_leftpad is not None:
         raise NotImplementedError("Turing KV-cache does not support cache_leftpad yet")
-    if tuple(window_size) != (-1, -1):
-        raise NotImplementedError("Turing KV-cache does not support local window attention yet")
-    if softcap != 0.0:
-        raise NotImplementedError("Turing KV-cache does not support softcap yet")
+    if len(tuple(window_size)) != 2 or not all(isinstance(w, int) for w in window_size):
+        raise TypeError("window_size must be a pair of ints")
+    if not math.isfinite(softcap):
+        raise ValueError("softcap must be finite")
     if alibi_slopes is not None:
         raise NotImplementedError("Turing KV-cache does not support ALiBi yet")
 
@@ -421,8 +425,12 @@ def flash_attn_with_kvcache(
 
     Supports contiguous caches (optionally remapped by cache_batch_idx), paged
     caches via block_table, in-place append of k/v at cache_seqlens and split-KV
-    (num_splits, 0 = heuristic).  Rotary, ALiBi, local windows, softcap and
-    cache_leftpad raise NotImplementedError, as in the reference.
+    (num_splits, 0 = heuristic).  Rotary, ALiBi and cache_leftpad raise
+    NotImplementedError, as in the reference.  Beyond the reference (which
+    rejects them), window_size and softcap work with upstream FlashAttention's
+    semantics: query i, at key position p = i + L - seqlen_q, sees keys
+    [p - left, p + right] (-1: unbounded; causal caps the right side at p), and
+    softcap > 0 replaces each scaled score x by softcap * tanh(x / softcap).
 
     validate (after the reference's arguments): True checks the cache capacity
     and cache_batch_idx on the host, raising at once as the reference does (two
@@ -496,6 +504,6 @@ def flash_attn_with_kvcache(
     status = None if validate else _kv_status(q.device)
     out, lse = _flash_attn_kvcache_forward(
         q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale, causal, num_splits,
-        status,
+        status, tuple(window_size), softcap,
     )
     return (out, lse) if return_softmax_lse else out

@@ -139,6 +139,15 @@ typedef struct fa_kvcache_args {
     int32_t cache_capacity;         /* tokens one sequence's cache holds (paged: pages * page size) */
     int32_t cache_batch;            /* rows of a contiguous cache (bounds cache_batch_idx)         */
     int32_t *status;                /* device int32 error word, or NULL                            */
+    /* Upstream FlashAttention options the reference's signature takes but rejects
+     * (flash_attention_interface.py:617-634), with upstream's semantics: query i
+     * (at key position p = i + L - seqlen_q) sees keys [p - window_left, p + window_right]
+     * (a negative bound is unbounded; causal also caps the right side at p), and
+     * softcap > 0 replaces the scaled score x by softcap * tanh(x / softcap).
+     * Zero-initialised, both are off. */
+    int32_t local_window;           /* 1: apply window_left / window_right; 0: no window */
+    int32_t window_left, window_right;
+    float softcap;                  /* > 0: softcapping on                                          */
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);

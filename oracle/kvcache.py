@@ -4,6 +4,14 @@ Restates the reference's own Python math path for ``flash_attn_with_kvcache``
 (flash_attention_interface.py:642-776) and the split / combine arithmetic of
 csrc/flash_attn/src/kvcache_native.cu:191-193 (split bounds), :676-729
 (log-sum-exp combine) and :782-871 (paged append).
+
+Local windows and softcap, which the reference's signature takes but rejects
+(flash_attention_interface.py:617-634, "the signature matches upstream
+FlashAttention"), follow upstream FlashAttention's documented semantics:
+query i (aligned bottom-right, at key position i + L - sq) sees keys
+[i + L - sq - left, i + L - sq + right] (a negative bound is unbounded; causal
+means right = 0), and softcap c > 0 replaces the scaled score s * scale by
+c * tanh(s * scale / c).
 """
 
 from typing import List, Optional, Tuple
@@ -130,6 +138,8 @@ def splitkv_attention(
     causal: bool,
     num_splits: int,
     dtype: torch.dtype = torch.float32,
+    window: Tuple[int, int] = (-1, -1),
+    softcap: float = 0.0,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Split-KV attention over materialised caches, per batch row
     (flash_attention_interface.py:731-776): each split is a separate softmax
@@ -137,6 +147,7 @@ def splitkv_attention(
 
     q [b, sq, h, d]; k_used/v_used [b, >=max_len, hk, d]; causal keeps key j for
     query i iff j <= i + L - sq with L = seqlens[b] (kvcache_native.cu:347).
+    ``window`` (left, right) and ``softcap`` as in the module docstring.
     Returns (out [b, sq, h, d] in ``dtype``, lse [b, h, sq] in ``dtype``)."""
     b, sq, h, d = q.shape
     hk = k_used.shape[2]
@@ -149,9 +160,19 @@ def splitkv_attention(
         vi = v_used[bi, :n].to(dtype).repeat_interleave(groups, dim=1).transpose(0, 1)
         splits = max(1, min(num_splits, n)) if num_splits > 0 else 1
         keep = causal_keep(sq, n) if causal else torch.ones((sq, n), dtype=torch.bool)
+        left, right = window
+        if left >= 0 or right >= 0:
+            pos = torch.arange(sq)[:, None] + n - sq  # the query's own key position
+            j = torch.arange(n)[None, :]
+            if left >= 0:
+                keep = keep & (j >= pos - left)
+            if right >= 0:
+                keep = keep & (j <= pos + right)
         parts_o, parts_l = [], []
         for s0, s1 in split_bounds(n, splits):
             sc = torch.matmul(qi, ki[:, s0:s1].transpose(-1, -2).contiguous()) * softmax_scale
+            if softcap > 0:
+                sc = softcap * torch.tanh(sc / softcap)
             sc = sc.masked_fill(~keep[:, s0:s1], float("-inf"))
             any_row = torch.isfinite(sc).any(dim=-1, keepdim=True) if s1 > s0 else torch.zeros(
                 (h, sq, 1), dtype=torch.bool

@@ -96,8 +96,6 @@ def test_rejects_capacity_overrun():
     [
         (dict(rotary_cos=_t(8, 32), rotary_sin=_t(8, 32)), "rotary embeddings"),
         (dict(cache_leftpad=torch.zeros(1, dtype=torch.int32)), "cache_leftpad"),
-        (dict(window_size=(4, 0)), "local window attention"),
-        (dict(softcap=30.0), "softcap"),
         (dict(alibi_slopes=_t(4)), "ALiBi"),
     ],
 )
@@ -105,6 +103,20 @@ def test_explicit_feature_rejections_come_first(kwargs, msg):
     # head_dim 96 and unpaired k would also be errors: the feature check wins.
     with pytest.raises(NotImplementedError, match=msg):
         fai.flash_attn_with_kvcache(_t(1, 2, 4, 96), _t(1, 8, 2, 96), _t(1, 8, 2, 96), k=_t(1, 1, 2, 96), **kwargs)
+
+
+@pytest.mark.parametrize("kwargs", [dict(window_size=(4, 0)), dict(softcap=30.0), dict(window_size=(-1, 2), softcap=5)])
+def test_window_and_softcap_are_accepted(kwargs):
+    # The reference rejects these (interface.py:617-634); here they pass the
+    # Python checks (upstream FlashAttention's semantics) and reach the next
+    # check, the device of the CPU tensors.
+    with pytest.raises(RuntimeError, match="must be CUDA tensors"):
+        fai.flash_attn_with_kvcache(_t(1, 2, 4, 64), _t(1, 8, 2, 64), _t(1, 8, 2, 64),
+                                    cache_seqlens=torch.tensor([3], dtype=torch.int32), **kwargs)
+    with pytest.raises(TypeError, match="window_size must be a pair of ints"):
+        fai.flash_attn_with_kvcache(_t(1, 2, 4, 64), _t(1, 8, 2, 64), _t(1, 8, 2, 64), window_size=(1.5, 0))
+    with pytest.raises(ValueError, match="softcap must be finite"):
+        fai.flash_attn_with_kvcache(_t(1, 2, 4, 64), _t(1, 8, 2, 64), _t(1, 8, 2, 64), softcap=float("inf"))
 
 
 def test_pairing_checked_before_head_dim():

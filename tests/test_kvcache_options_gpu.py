@@ -1,0 +1,79 @@
+"""Local windows and softcap in flash_attn_with_kvcache (upstream FlashAttention
+semantics; the reference's signature takes these but rejects them,
+flash_attention_interface.py:617-634) against the extended CPU oracle.
+
+Bound: as for the other KV-cache outputs (the kernels are fp32 until the final
+fp16 rounding), 2x the error of the fp16-rounded oracle; LSE to fp32 precision.
+Cases cover paged and contiguous / remapped caches, one and several query
+tokens (several go through the split kernel too), GQA, explicit and heuristic
+split counts, and a long cache whose splits mostly fall outside the window
+(the kernel skips those tiles)."""
+
+import pytest
+import torch
+
+import flash_attention_interface as fai
+from helpers import assert_2x, assert_lse, randn16
+from oracle import kvcache as okv
+
+CASES = [
+    # b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap
+    (3, 1, 8, 2, 128, 1024, 1, True, 0, True, False, (100, -1), 0.0),
+    (3, 1, 8, 2, 128, 1024, 1, True, 4, False, False, (0, 0), 0.0),
+    (2, 4, 8, 8, 64, 512, 4, True, 1, False, True, (37, 0), 0.0),
+    (2, 4, 8, 8, 64, 512, 4, False, 2, False, False, (5, 3), 0.0),
+    (3, 1, 8, 2, 128, 1024, 1, True, 8, True, False, (-1, -1), 30.0),
+    (2, 3, 6, 2, 64, 512, 3, True, 0, False, True, (64, -1), 5.0),
+    (2, 1, 8, 2, 128, 4096, 1, True, 16, True, False, (300, -1), 0.0),
+    (2, 5, 4, 1, 128, 768, 0, True, 3, False, False, (2000, 1), 1.5),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,sq,h,hk,hd,cap,new,causal,splits,paged,remap,window,softcap", CASES)
+def test_kvcache_window_softcap(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap):
+    g = torch.Generator().manual_seed(8000 + b * 13 + sq + hd + cap // 256)
+    rows = b + 2 if remap else b
+    kc = randn16((rows, cap, hk, hd), g)
+    vc = randn16((rows, cap, hk, hd), g)
+    q = randn16((b, sq, h, hd), g)
+    k = randn16((b, new, hk, hd), g) if new else None
+    v = randn16((b, new, hk, hd), g) if new else None
+    seqlens = torch.randint(max(0, sq - new), cap - new + 1, (b,), generator=g, dtype=torch.int32)
+    seqlens[0] = cap - new
+    batch_idx = torch.randperm(rows, generator=g)[:b].to(torch.int32) if remap else None
+    table = None
+    kcp, vcp = kc, vc
+    if paged:
+        nb = cap // 256
+        table = torch.randperm(b * nb, generator=g).reshape(b, nb).to(torch.int32)
+        kcp = torch.zeros((b * nb, 256, hk, hd), dtype=torch.float16)
+        vcp = torch.zeros_like(kcp)
+        for bi in range(b):
+            for j in range(nb):
+                kcp[table[bi, j]] = kc[bi, j * 256 : (j + 1) * 256]
+                vcp[table[bi, j]] = vc[bi, j * 256 : (j + 1) * 256]
+    kcd, vcd = kcp.clone().to(device), vcp.clone().to(device)
+    out, lse = fai.flash_attn_with_kvcache(
+        q.to(device), kcd, vcd, None if k is None else k.to(device), None if v is None else v.to(device),
+        cache_seqlens=seqlens.to(device), cache_batch_idx=None if batch_idx is None else batch_idx.to(device),
+        block_table=None if table is None else table.to(device), causal=causal, num_splits=splits,
+        window_size=window, softcap=softcap, return_softmax_lse=True,
+    )
+    torch.cuda.synchronize()
+    # Oracle: append, materialise the logical caches, attend.
+    kr, vr = kcp.clone(), vcp.clone()
+    if k is not None:
+        if table is None:
+            okv.append_contiguous(kr, vr, k, v, seqlens, batch_idx)
+        else:
+            okv.append_paged(kr, vr, k, v, seqlens, table)
+    assert torch.equal(kcd.cpu(), kr) and torch.equal(vcd.cpu(), vr), "append differs from the oracle"
+    ends = seqlens + new
+    ku, vu = okv.materialize(kr, vr, ends, batch_idx, table)
+    # Upstream's normalisation of bounds at least the capacity.
+    w = tuple(-1 if x >= cap else x for x in window)
+    o_ref, l_ref = okv.splitkv_attention(q, ku, vu, ends, hd ** -0.5, causal, max(splits, 1), window=w,
+                                         softcap=softcap)
+    assert_2x("out", out.cpu(), o_ref, o_ref.to(torch.float16))
+    assert_lse(lse.cpu(), l_ref)

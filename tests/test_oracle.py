@@ -265,6 +265,57 @@ def test_splitkv_equals_unsplit_and_dense(causal):
         assert torch.allclose(o1[bi], bo[0], atol=1e-12) and torch.allclose(l1[bi], bl[0], atol=1e-12)
 
 
+def test_splitkv_window_closed_forms():
+    # Window (0, 0): each query sees exactly the key at its own aligned
+    # position i + L - sq, so O is that key's V and LSE its scaled score.
+    q = _rand((2, 3, 2, 8), 40)
+    ku, vu = _rand((2, 20, 2, 8), 41), _rand((2, 20, 2, 8), 42)
+    lens = torch.tensor([20, 7], dtype=torch.int32)
+    o, l = okv.splitkv_attention(q, ku, vu, lens, 0.4, False, 3, dtype=D64, window=(0, 0))
+    for bi, n in enumerate(lens.tolist()):
+        for i in range(3):
+            j = i + n - 3
+            assert torch.allclose(o[bi, i], vu[bi, j], atol=1e-12)
+            sc = (q[bi, i] * ku[bi, j]).sum(-1) * 0.4
+            assert torch.allclose(l[bi, :, i], sc, atol=1e-12)
+    # A left window of w with causal on equals plain attention over the last
+    # w + 1 keys (one query): the window is a slice of the cache.
+    q1 = _rand((2, 1, 2, 8), 43)
+    for w in (0, 3, 19, 100):
+        ow, lw = okv.splitkv_attention(q1, ku, vu, lens, 0.4, True, 2, dtype=D64, window=(w, -1))
+        for bi, n in enumerate(lens.tolist()):
+            lo = max(0, n - 1 - w)
+            kk, vv = ku[bi : bi + 1, lo:n], vu[bi : bi + 1, lo:n]
+            bo, bl = _brute_fwd(q1[bi : bi + 1], kk, vv, 0.4, True)
+            assert torch.allclose(ow[bi], bo[0], atol=1e-12) and torch.allclose(lw[bi], bl[0], atol=1e-12)
+    # A right bound of 0 is causal; wide windows change nothing.
+    oc, lc = okv.splitkv_attention(q, ku, vu, lens, 0.4, True, 2, dtype=D64)
+    or_, lr = okv.splitkv_attention(q, ku, vu, lens, 0.4, False, 2, dtype=D64, window=(-1, 0))
+    ow_, lw_ = okv.splitkv_attention(q, ku, vu, lens, 0.4, True, 2, dtype=D64, window=(50, 50))
+    assert torch.allclose(oc, or_, atol=1e-12) and torch.allclose(lc, lr, atol=1e-12)
+    assert torch.allclose(oc, ow_, atol=1e-12) and torch.allclose(lc, lw_, atol=1e-12)
+
+
+def test_splitkv_softcap_known_answers():
+    # One key: O = V whatever the cap; LSE = c * tanh(s * scale / c).
+    q = torch.tensor([[[[1.0, 2.0]]]], dtype=D64)
+    k = torch.tensor([[[[3.0, -0.5]], [[0.0, 0.0]]]], dtype=D64)
+    v = torch.tensor([[[[1.0, 5.0]], [[-2.0, 4.0]]]], dtype=D64)
+    o, l = okv.splitkv_attention(q, k, v, torch.tensor([1], dtype=torch.int32), 0.5, False, 1, dtype=D64, softcap=0.7)
+    assert torch.allclose(o[0, 0, 0], v[0, 0, 0]) and abs(l.item() - 0.7 * math.tanh(2.0 * 0.5 / 0.7)) < 1e-15
+    # Two keys with scores 2 and 0: weights exp(c tanh(2 * .5 / c)) : exp(0).
+    o, l = okv.splitkv_attention(q, k, v, torch.tensor([2], dtype=torch.int32), 0.5, False, 2, dtype=D64, softcap=0.7)
+    a = math.exp(0.7 * math.tanh(1.0 / 0.7))
+    assert torch.allclose(o[0, 0, 0], torch.tensor([(a * 1.0 - 2.0) / (a + 1), (a * 5.0 + 4.0) / (a + 1)], dtype=D64))
+    assert abs(l.item() - math.log(a + 1.0)) < 1e-14
+    # A huge cap is no cap.
+    qq, kk, vv = _rand((2, 3, 4, 8), 44), _rand((2, 30, 2, 8), 45), _rand((2, 30, 2, 8), 46)
+    lens = torch.tensor([30, 11], dtype=torch.int32)
+    o1, l1 = okv.splitkv_attention(qq, kk, vv, lens, 0.3, True, 3, dtype=D64)
+    o2, l2 = okv.splitkv_attention(qq, kk, vv, lens, 0.3, True, 3, dtype=D64, softcap=1e7)
+    assert torch.allclose(o1, o2, atol=1e-9) and torch.allclose(l1, l2, atol=1e-9)
+
+
 # --------------------------------------------------------------------------- twin
 
 
