@@ -143,8 +143,8 @@ __device__ __forceinline__ float tanh_fast(float x) {
 // unclaimed item from a device counter, so no workgroup is relaunched and
 // the items are dealt out greedily in that order.  The counter
 // (batch_order[batch]) is zeroed by kv_order_kernel on the same stream.
-// EXT switches on the local window and softcap options (a separate instance,
-// so the plain kernel carries none of their work).
+// EXT switches on the local window, softcap, ALiBi and cache_leftpad options
+// (a separate instance, so the plain kernel carries none of their work).
 template <int HD, bool DYN, bool EXT>
 __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a,
                                                                                    const int row_tiles,
@@ -173,7 +173,10 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         if (sq.err && a.status && tid == 0) atomicOr(a.status, sq.err);
         const int L = sq.err ? 0 : sq.L0 + a.seqlen_new;
         const int S = a.num_splits;
-        const int s0 = int((int64_t(L) * split) / S), s1 = int((int64_t(L) * (split + 1)) / S);
+        // Valid keys [kstart, L): cache_leftpad moves the start, positions stay.
+        const int kstart = EXT && a.cache_leftpad ? min(max(a.cache_leftpad[b], 0), L) : 0;
+        const int s0 = kstart + int((int64_t(L - kstart) * split) / S);
+        const int s1 = kstart + int((int64_t(L - kstart) * (split + 1)) / S);
         const int cache_row = sq.row;
 
         // This lane's query row.
@@ -202,10 +205,15 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
 
         const bool neg = a.softmax_scale < 0.f;
         const bool capped = EXT && a.softcap > 0.f;
-        // The exponent multiplier: scale * log2(e), or log2(e) for softcapped
-        // scores (already scaled); cap_in = scale / softcap.
-        const float cscale = capped ? kLog2e : fabsf(a.softmax_scale) * kLog2e;
+        const bool alibi = EXT && a.alibi_slopes != nullptr;
+        // Softcapped or biased scores are formed in natural units (scaled), so
+        // the exponent multiplier is log2(e) for them and scale * log2(e)
+        // otherwise; cap_in = scale / softcap.
+        const bool natural = capped || alibi;
+        const float cscale = natural ? kLog2e : fabsf(a.softmax_scale) * kLog2e;
         const float cap_in = capped ? fabsf(a.softmax_scale) / a.softcap : 0.f;
+        const float slope = alibi ? a.alibi_slopes[int64_t(b) * a.alibi_batch_stride + hq] : 0.f;
+        const int qkey = qpos + L - a.seqlen_q;  // the query's own key position (ALiBi distance origin)
         f16x8 qB[HD / 16];
         {
             const f16 *qp = (const f16 *)a.q.ptr + int64_t(b) * a.q.batch_stride + int64_t(qpos) * a.q.row_stride +
@@ -301,9 +309,14 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
     #pragma unroll
             for (int g = 1; g < HD / 16; ++g) s = mfma32(ka[g], qB[g], s);
             if constexpr (EXT) {
-                if (capped) {
+                if (natural) {
+                    const float sc = fabsf(a.softmax_scale);
     #pragma unroll
-                    for (int r = 0; r < 16; ++r) s[r] = a.softcap * tanh_fast(s[r] * cap_in);
+                    for (int r = 0; r < 16; ++r) {
+                        float x = capped ? a.softcap * tanh_fast(s[r] * cap_in) : s[r] * sc;
+                        if (alibi) x -= slope * float(abs(qkey - (p0 + acc_lrow(r, hh))));
+                        s[r] = x;
+                    }
                 }
             }
             float mx = -INFINITY;
@@ -609,7 +622,7 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     } else {
         run.batch_order = nullptr;  // natural order
     }
-    const bool ext = a.local_window || a.softcap > 0.f;
+    const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes;
     auto go = [&](auto hd_tag, auto dyn_tag, auto ext_tag) {
         constexpr int HD = decltype(hd_tag)::value;
         constexpr bool DYN = decltype(dyn_tag)::value, EXT = decltype(ext_tag)::value;

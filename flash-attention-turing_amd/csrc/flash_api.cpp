@@ -331,11 +331,11 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     (void)rotary_interleaved;
     TORCH_CHECK(!rotary_cos.has_value() && !rotary_sin.has_value(),
                 "Turing KV-cache does not support rotary embeddings yet");
-    TORCH_CHECK(!cache_leftpad.has_value(), "Turing KV-cache does not support cache_leftpad yet");
-    TORCH_CHECK(!alibi_slopes.has_value(), "Turing KV-cache does not support ALiBi yet");
+
     TORCH_CHECK(!out_opt.has_value(), "Turing KV-cache does not support a preallocated output tensor yet");
-    // Local windows and softcap (rejected by the reference, flash_api.cpp:530-539)
-    // take upstream FlashAttention's semantics; they run in the split kernel.
+    // Local windows, softcap, ALiBi and cache_leftpad (rejected by the
+    // reference, flash_api.cpp:530-539) take upstream FlashAttention's
+    // semantics; they run in the split kernel.
     TORCH_CHECK(std::isfinite(softcap), "softcap must be finite");
     TORCH_CHECK(num_splits >= 0, "num_splits must be non-negative");
 
@@ -482,7 +482,26 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     a.window_left = window_size_left;
     a.window_right = window_size_right;
     a.softcap = softcap > 0.f ? softcap : 0.f;
-    const bool options = a.local_window || a.softcap > 0.f;
+    if (cache_leftpad.has_value()) {
+        const at::Tensor &lp = *cache_leftpad;
+        TORCH_CHECK(lp.is_cuda() && lp.device() == q.device(), "cache_leftpad must be a CUDA tensor on the device of q");
+        TORCH_CHECK(lp.scalar_type() == at::kInt, "cache_leftpad must have dtype int32");
+        TORCH_CHECK(lp.dim() == 1 && lp.size(0) == batch_size && lp.is_contiguous(),
+                    "cache_leftpad must be a contiguous tensor of shape [batch_size]");
+        a.cache_leftpad = lp.data_ptr<int32_t>();
+    }
+    if (alibi_slopes.has_value()) {
+        const at::Tensor &al = *alibi_slopes;
+        TORCH_CHECK(al.is_cuda() && al.device() == q.device(), "alibi_slopes must be a CUDA tensor on the device of q");
+        TORCH_CHECK(al.scalar_type() == at::kFloat, "ALiBi slopes must have dtype fp32");
+        TORCH_CHECK(al.stride(-1) == 1, "ALiBi slopes tensor must have contiguous last dimension");
+        TORCH_CHECK((al.dim() == 1 && al.size(0) == num_heads) ||
+                        (al.dim() == 2 && al.size(0) == batch_size && al.size(1) == num_heads),
+                    "ALiBi slopes must have shape (num_heads) or (batch_size, num_heads)");
+        a.alibi_slopes = al.data_ptr<float>();
+        a.alibi_batch_stride = al.dim() == 2 ? al.stride(0) : 0;
+    }
+    const bool options = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes;
 
     check_rc(fa_kv_append(&a, stream), "fa_kv_append");
 

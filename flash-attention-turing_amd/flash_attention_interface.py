@@ -91,19 +91,22 @@ def _flash_attn_varlen_backward(
 def _flash_attn_kvcache_forward(
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale: float, causal: bool,
     num_splits: int, status: Optional[torch.Tensor] = None, window_size: Tuple[int, int] = (-1, -1),
-    softcap: float = 0.0,
+    softcap: float = 0.0, cache_leftpad: Optional[torch.Tensor] = None, alibi_slopes: Optional[torch.Tensor] = None,
 ):
-    tensors = (q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table)
-    q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table = (maybe_contiguous(t) for t in tensors)
-    # The 20-argument binding of flash_api.cpp:508-528; rotary, leftpad, ALiBi
-    # and a preallocated out are passed as "absent".
+    tensors = (q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, cache_leftpad, alibi_slopes)
+    q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, cache_leftpad, alibi_slopes = (
+        maybe_contiguous(t) for t in tensors
+    )
+    # The 20-argument binding of flash_api.cpp:508-528; rotary and a
+    # preallocated out are passed as "absent".
     out, lse = flash_attn_gpu.fwd_kvcache(
         q, k_cache, v_cache, k, v, cache_seqlens,
         None, None,            # rotary_cos, rotary_sin
         cache_batch_idx,
-        None,                  # cache_leftpad
+        cache_leftpad,
         block_table,
-        None, None,            # alibi_slopes, out
+        alibi_slopes,
+        None,                  # out
         softmax_scale, causal,
         int(window_size[0]), int(window_size[1]),
         float(softcap),
@@ -326,18 +329,19 @@ def flash_attn_varlen_kvpacked_func(
 
 
 def _validate_unsupported_kvcache_args(rotary_cos, rotary_sin, cache_leftpad, window_size, softcap, alibi_slopes):
-    # interface.py:617-634 rejects all five; local windows and softcap are
-    # supported here (upstream FlashAttention's semantics), the rest are not.
+    # interface.py:617-634 rejects all five; local windows, softcap, ALiBi and
+    # cache_leftpad are supported here (upstream FlashAttention's semantics),
+    # rotary embeddings are not.
     if rotary_cos is not None or rotary_sin is not None:
         raise NotImplementedError("Turing KV-cache does not support rotary embeddings yet")
-    if cache_leftpad is not None:
-        raise NotImplementedError("Turing KV-cache does not support cache_leftpad yet")
     if len(tuple(window_size)) != 2 or not all(isinstance(w, int) for w in window_size):
         raise TypeError("window_size must be a pair of ints")
     if not math.isfinite(softcap):
         raise ValueError("softcap must be finite")
-    if alibi_slopes is not None:
-        raise NotImplementedError("Turing KV-cache does not support ALiBi yet")
+    if cache_leftpad is not None and (not isinstance(cache_leftpad, torch.Tensor) or cache_leftpad.dtype != torch.int32):
+        raise TypeError("cache_leftpad must be a torch.int32 tensor")
+    if alibi_slopes is not None and (not isinstance(alibi_slopes, torch.Tensor) or alibi_slopes.dtype != torch.float32):
+        raise TypeError("alibi_slopes must be a torch.float32 tensor")
 
 
 def _validate_supported_head_dim(head_dim: int) -> None:
@@ -425,12 +429,14 @@ def flash_attn_with_kvcache(
 
     Supports contiguous caches (optionally remapped by cache_batch_idx), paged
     caches via block_table, in-place append of k/v at cache_seqlens and split-KV
-    (num_splits, 0 = heuristic).  Rotary, ALiBi and cache_leftpad raise
-    NotImplementedError, as in the reference.  Beyond the reference (which
-    rejects them), window_size and softcap work with upstream FlashAttention's
-    semantics: query i, at key position p = i + L - seqlen_q, sees keys
-    [p - left, p + right] (-1: unbounded; causal caps the right side at p), and
-    softcap > 0 replaces each scaled score x by softcap * tanh(x / softcap).
+    (num_splits, 0 = heuristic).  Rotary embeddings raise NotImplementedError,
+    as in the reference.  Beyond the reference (which rejects them),
+    window_size, softcap, alibi_slopes and cache_leftpad work with upstream
+    FlashAttention's semantics: query i, at key position p = i + L - seqlen_q,
+    sees keys [p - left, p + right] (-1: unbounded; causal caps the right side
+    at p); softcap > 0 replaces each scaled score x by softcap * tanh(x / softcap);
+    ALiBi (fp32 slopes [nheads] or [batch, nheads]) adds -slope * |p - j| to the
+    score of key j; keys before cache_leftpad[b] (int32 [batch]) do not exist.
 
     validate (after the reference's arguments): True checks the cache capacity
     and cache_batch_idx on the host, raising at once as the reference does (two
@@ -504,6 +510,6 @@ def flash_attn_with_kvcache(
     status = None if validate else _kv_status(q.device)
     out, lse = _flash_attn_kvcache_forward(
         q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale, causal, num_splits,
-        status, tuple(window_size), softcap,
+        status, tuple(window_size), softcap, cache_leftpad, alibi_slopes,
     )
     return (out, lse) if return_softmax_lse else out

@@ -143,11 +143,15 @@ typedef struct fa_kvcache_args {
      * (flash_attention_interface.py:617-634), with upstream's semantics: query i
      * (at key position p = i + L - seqlen_q) sees keys [p - window_left, p + window_right]
      * (a negative bound is unbounded; causal also caps the right side at p), and
-     * softcap > 0 replaces the scaled score x by softcap * tanh(x / softcap).
-     * Zero-initialised, both are off. */
+     * softcap > 0 replaces the scaled score x by softcap * tanh(x / softcap),
+     * ALiBi adds -slope[h] * |p - j| to the score of key j, and key j < cache_leftpad[b]
+     * does not exist for sequence b (positions unchanged).  Zero-initialised, all are off. */
     int32_t local_window;           /* 1: apply window_left / window_right; 0: no window */
     int32_t window_left, window_right;
     float softcap;                  /* > 0: softcapping on                                          */
+    const int32_t *cache_leftpad;   /* [batch] first valid key of each sequence, or NULL            */
+    const float *alibi_slopes;      /* fp32 [nheads] (batch stride 0) or [batch][nheads], or NULL   */
+    int64_t alibi_batch_stride;
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);

@@ -10,8 +10,10 @@ Local windows and softcap, which the reference's signature takes but rejects
 FlashAttention"), follow upstream FlashAttention's documented semantics:
 query i (aligned bottom-right, at key position i + L - sq) sees keys
 [i + L - sq - left, i + L - sq + right] (a negative bound is unbounded; causal
-means right = 0), and softcap c > 0 replaces the scaled score s * scale by
-c * tanh(s * scale / c).
+means right = 0), softcap c > 0 replaces the scaled score s * scale by
+c * tanh(s * scale / c), ALiBi adds -slope_h * |i + L - sq - j| to the score
+fed to the softmax (slopes [h] or [b, h]), and cache_leftpad[b] is the first
+valid key of sequence b (positions unchanged).
 """
 
 from typing import List, Optional, Tuple
@@ -140,6 +142,8 @@ def splitkv_attention(
     dtype: torch.dtype = torch.float32,
     window: Tuple[int, int] = (-1, -1),
     softcap: float = 0.0,
+    alibi_slopes: Optional[torch.Tensor] = None,
+    leftpad: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Split-KV attention over materialised caches, per batch row
     (flash_attention_interface.py:731-776): each split is a separate softmax
@@ -147,7 +151,8 @@ def splitkv_attention(
 
     q [b, sq, h, d]; k_used/v_used [b, >=max_len, hk, d]; causal keeps key j for
     query i iff j <= i + L - sq with L = seqlens[b] (kvcache_native.cu:347).
-    ``window`` (left, right) and ``softcap`` as in the module docstring.
+    ``window`` (left, right), ``softcap``, ``alibi_slopes`` and ``leftpad`` as in
+    the module docstring.
     Returns (out [b, sq, h, d] in ``dtype``, lse [b, h, sq] in ``dtype``)."""
     b, sq, h, d = q.shape
     hk = k_used.shape[2]
@@ -168,11 +173,21 @@ def splitkv_attention(
                 keep = keep & (j >= pos - left)
             if right >= 0:
                 keep = keep & (j <= pos + right)
+        if leftpad is not None:
+            keep = keep & (torch.arange(n)[None, :] >= int(leftpad[bi]))
+        bias = None
+        if alibi_slopes is not None:
+            sl = alibi_slopes[bi] if alibi_slopes.dim() == 2 else alibi_slopes
+            pos = torch.arange(sq)[:, None] + n - sq
+            dist = (pos - torch.arange(n)[None, :]).abs().to(dtype)
+            bias = -sl.to(dtype)[:, None, None] * dist[None]  # h sq n
         parts_o, parts_l = [], []
         for s0, s1 in split_bounds(n, splits):
             sc = torch.matmul(qi, ki[:, s0:s1].transpose(-1, -2).contiguous()) * softmax_scale
             if softcap > 0:
                 sc = softcap * torch.tanh(sc / softcap)
+            if bias is not None:
+                sc = sc + bias[:, :, s0:s1]
             sc = sc.masked_fill(~keep[:, s0:s1], float("-inf"))
             any_row = torch.isfinite(sc).any(dim=-1, keepdim=True) if s1 > s0 else torch.zeros(
                 (h, sq, 1), dtype=torch.bool

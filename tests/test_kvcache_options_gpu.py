@@ -1,6 +1,7 @@
-"""Local windows and softcap in flash_attn_with_kvcache (upstream FlashAttention
-semantics; the reference's signature takes these but rejects them,
-flash_attention_interface.py:617-634) against the extended CPU oracle.
+"""Local windows, softcap, ALiBi and cache_leftpad in flash_attn_with_kvcache
+(upstream FlashAttention semantics; the reference's signature takes these but
+rejects them, flash_attention_interface.py:617-634) against the extended CPU
+oracle.
 
 Bound: as for the other KV-cache outputs (the kernels are fp32 until the final
 fp16 rounding), 2x the error of the fp16-rounded oracle; LSE to fp32 precision.
@@ -32,7 +33,29 @@ CASES = [
 @pytest.mark.gpu
 @pytest.mark.parametrize("b,sq,h,hk,hd,cap,new,causal,splits,paged,remap,window,softcap", CASES)
 def test_kvcache_window_softcap(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap):
-    g = torch.Generator().manual_seed(8000 + b * 13 + sq + hd + cap // 256)
+    _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, None, False)
+
+
+CASES_ALIBI_LEFTPAD = [
+    # b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad
+    (3, 1, 8, 2, 128, 1024, 1, True, 0, True, False, (-1, -1), 0.0, "h", False),
+    (2, 4, 8, 8, 64, 512, 4, False, 2, False, True, (-1, -1), 0.0, "bh", False),
+    (3, 1, 8, 2, 128, 1024, 1, True, 4, False, False, (-1, -1), 0.0, None, True),
+    (2, 4, 6, 2, 64, 512, 4, True, 1, False, True, (-1, -1), 0.0, None, True),
+    (2, 3, 8, 2, 128, 768, 3, True, 3, True, False, (50, -1), 10.0, "h", True),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,sq,h,hk,hd,cap,new,causal,splits,paged,remap,window,softcap,alibi,leftpad",
+                         CASES_ALIBI_LEFTPAD)
+def test_kvcache_alibi_leftpad(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap,
+                               alibi, leftpad):
+    _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad)
+
+
+def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad):
+    g = torch.Generator().manual_seed(8000 + b * 13 + sq + hd + cap // 256 + (alibi is not None) + 2 * leftpad)
     rows = b + 2 if remap else b
     kc = randn16((rows, cap, hk, hd), g)
     vc = randn16((rows, cap, hk, hd), g)
@@ -42,6 +65,12 @@ def test_kvcache_window_softcap(device, b, sq, h, hk, hd, cap, new, causal, spli
     seqlens = torch.randint(max(0, sq - new), cap - new + 1, (b,), generator=g, dtype=torch.int32)
     seqlens[0] = cap - new
     batch_idx = torch.randperm(rows, generator=g)[:b].to(torch.int32) if remap else None
+    slopes = None
+    if alibi == "h":
+        slopes = torch.rand((h,), generator=g) * 0.5
+    elif alibi == "bh":
+        slopes = torch.rand((b, h), generator=g) * 0.5
+    lpad = torch.randint(0, 64, (b,), generator=g, dtype=torch.int32) if leftpad else None
     table = None
     kcp, vcp = kc, vc
     if paged:
@@ -59,6 +88,8 @@ def test_kvcache_window_softcap(device, b, sq, h, hk, hd, cap, new, causal, spli
         cache_seqlens=seqlens.to(device), cache_batch_idx=None if batch_idx is None else batch_idx.to(device),
         block_table=None if table is None else table.to(device), causal=causal, num_splits=splits,
         window_size=window, softcap=softcap, return_softmax_lse=True,
+        alibi_slopes=None if slopes is None else slopes.to(device),
+        cache_leftpad=None if lpad is None else lpad.to(device),
     )
     torch.cuda.synchronize()
     # Oracle: append, materialise the logical caches, attend.
@@ -74,6 +105,6 @@ def test_kvcache_window_softcap(device, b, sq, h, hk, hd, cap, new, causal, spli
     # Upstream's normalisation of bounds at least the capacity.
     w = tuple(-1 if x >= cap else x for x in window)
     o_ref, l_ref = okv.splitkv_attention(q, ku, vu, ends, hd ** -0.5, causal, max(splits, 1), window=w,
-                                         softcap=softcap)
+                                         softcap=softcap, alibi_slopes=slopes, leftpad=lpad)
     assert_2x("out", out.cpu(), o_ref, o_ref.to(torch.float16))
     assert_lse(lse.cpu(), l_ref)

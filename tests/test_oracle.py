@@ -316,6 +316,40 @@ def test_splitkv_softcap_known_answers():
     assert torch.allclose(o1, o2, atol=1e-9) and torch.allclose(l1, l2, atol=1e-9)
 
 
+def test_splitkv_alibi_and_leftpad_known_answers():
+    # ALiBi with all scores 0 (q = 0), causal, one query at position L - 1:
+    # weights exp(-slope * (L - 1 - j)), a geometric sequence.
+    L, slope = 5, 0.7
+    q = torch.zeros((1, 1, 2, 4), dtype=D64)
+    k = _rand((1, L, 1, 4), 47)
+    v = _rand((1, L, 1, 4), 48)
+    slopes = torch.tensor([slope, 0.0], dtype=D64)
+    o, l = okv.splitkv_attention(q, k, v, torch.tensor([L], dtype=torch.int32), 0.5, True, 2, dtype=D64,
+                                 alibi_slopes=slopes)
+    w = torch.tensor([math.exp(-slope * (L - 1 - j)) for j in range(L)], dtype=D64)
+    assert torch.allclose(o[0, 0, 0], (w[:, None] * v[0, :, 0]).sum(0) / w.sum(), atol=1e-13)
+    assert abs(l[0, 0, 0].item() - math.log(w.sum().item())) < 1e-13
+    assert torch.allclose(o[0, 0, 1], v[0, :, 0].mean(0), atol=1e-13)  # slope 0: plain mean
+    # Per-batch slopes [b, h] equal the per-head form row by row; non-causal
+    # bias is symmetric in |i + L - sq - j|.
+    qq, kk, vv = _rand((2, 3, 4, 8), 49), _rand((2, 12, 2, 8), 50), _rand((2, 12, 2, 8), 51)
+    lens = torch.tensor([12, 6], dtype=torch.int32)
+    sl2 = torch.rand((2, 4), generator=torch.Generator().manual_seed(52), dtype=D64)
+    ob, lb = okv.splitkv_attention(qq, kk, vv, lens, 0.3, False, 3, dtype=D64, alibi_slopes=sl2)
+    for bi in range(2):
+        oh, lh = okv.splitkv_attention(qq[bi : bi + 1], kk[bi : bi + 1], vv[bi : bi + 1], lens[bi : bi + 1], 0.3,
+                                       False, 1, dtype=D64, alibi_slopes=sl2[bi])
+        assert torch.allclose(ob[bi], oh[0], atol=1e-12) and torch.allclose(lb[bi], lh[0], atol=1e-12)
+    # cache_leftpad: keys before leftpad[b] do not exist; positions stay, so a
+    # causal query sees the slice [leftpad, i + L - sq].
+    lp = torch.tensor([4, 0], dtype=torch.int32)
+    o1, l1 = okv.splitkv_attention(qq, kk, vv, lens, 0.3, True, 2, dtype=D64, leftpad=lp)
+    for bi, n in enumerate(lens.tolist()):
+        a = int(lp[bi])
+        bo, bl = _brute_fwd(qq[bi : bi + 1], kk[bi : bi + 1, a:n], vv[bi : bi + 1, a:n], 0.3, True)
+        assert torch.allclose(o1[bi], bo[0], atol=1e-12) and torch.allclose(l1[bi], bl[0], atol=1e-12)
+
+
 # --------------------------------------------------------------------------- twin
 
 
