@@ -80,8 +80,52 @@ __device__ __forceinline__ KvSeq kv_seq(const fa_kvcache_args &a, int b) {
     return s;
 }
 
+// Rotary embedding of the 8 channels [c0, c0 + 8) of one row (c0 a multiple of
+// 8 below rotary_dim) at position pos: x holds them, row points at channel 0
+// of the row (the non-interleaved form reads the partner channels there).
+// Each output is x_a * cos - x_b * sin or x_a * sin + x_b * cos in fp32; the
+// products of fp16 values are exact in fp32, so it is the exact rotation of
+// the fp16 inputs rounded once to fp32, then to fp16.
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 rotary8(const fa_kvcache_args &a, const u32x4 x, const f16 *row, int c0, int pos) {
+    // Opaque to the optimiser: keeps the per-channel table addresses from being
+    // hoisted out of the split kernel's item loop, where they would stay live
+    // (in spilled registers) through it.
+    asm volatile("" : "+v"(c0));
+    const int half = a.rotary_dim / 2;
+    const int64_t base = int64_t(min(max(pos, 0), a.rotary_seqlen - 1)) * half;
+    const f16 *cs = (const f16 *)a.rotary_cos + base;
+    const f16 *sn = (const f16 *)a.rotary_sin + base;
+    const f16x8 xv = as_h8(x);
+    f16x8 r;
+    if (a.rotary_interleaved) {
+        const f16x4 c = *reinterpret_cast<const f16x4 *>(cs + c0 / 2);
+        const f16x4 s = *reinterpret_cast<const f16x4 *>(sn + c0 / 2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x0 = float(xv[2 * e]), x1 = float(xv[2 * e + 1]);
+            const float ce = float(c[e]), se = float(s[e]);
+            r[2 * e] = f16(x0 * ce - x1 * se);
+            r[2 * e + 1] = f16(x0 * se + x1 * ce);
+        }
+    } else {
+        const bool first = c0 < half;
+        const int j0 = first ? c0 : c0 - half;
+        const f16x8 pv = as_h8(ldg16(row + (first ? c0 + half : j0)));
+        const f16x8 c = as_h8(ldg16(cs + j0));
+        const f16x8 s = as_h8(ldg16(sn + j0));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float xe = float(xv[e]), pe = float(pv[e]), ce = float(c[e]), se = float(s[e]);
+            r[e] = f16(first ? xe * ce - pe * se : xe * ce + pe * se);
+        }
+    }
+    return __builtin_bit_cast(u32x4, r);
+}
+
 // ---------------------------------------------------------------------------
-// Append: one thread per 16-byte chunk of k_new / v_new.
+// Append: one thread per 16-byte chunk of k_new / v_new (with rotary_dim > 0,
+// the key chunks below rotary_dim are rotated at their position first).
 template <int HD>
 __global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a) {
     constexpr int KCH = HD / 8;
@@ -107,7 +151,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a)
                     int64_t(hk) * a.v_new.head_stride + 8 * c;
     f16 *kd = const_cast<f16 *>(kv_row_ptr(a.k_cache, a, b, cache_row, hk, pos)) + 8 * c;
     f16 *vd = const_cast<f16 *>(kv_row_ptr(a.v_cache, a, b, cache_row, hk, pos)) + 8 * c;
-    *reinterpret_cast<u32x4 *>(kd) = ldg16(ks);
+    u32x4 kx = ldg16(ks);
+    if (8 * c < a.rotary_dim) kx = rotary8(a, kx, ks - 8 * c, 8 * c, pos);
+    *reinterpret_cast<u32x4 *>(kd) = kx;
     *reinterpret_cast<u32x4 *>(vd) = ldg16(vs);
 }
 
@@ -143,7 +189,7 @@ __device__ __forceinline__ float tanh_fast(float x) {
 // unclaimed item from a device counter, so no workgroup is relaunched and
 // the items are dealt out greedily in that order.  The counter
 // (batch_order[batch]) is zeroed by kv_order_kernel on the same stream.
-// EXT switches on the local window, softcap, ALiBi and cache_leftpad options
+// EXT switches on the local window, softcap, ALiBi, cache_leftpad and rotary options
 // (a separate instance, so the plain kernel carries none of their work).
 template <int HD, bool DYN, bool EXT>
 __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a,
@@ -214,6 +260,9 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         const float cap_in = capped ? fabsf(a.softmax_scale) / a.softcap : 0.f;
         const float slope = alibi ? a.alibi_slopes[int64_t(b) * a.alibi_batch_stride + hq] : 0.f;
         const int qkey = qpos + L - a.seqlen_q;  // the query's own key position (ALiBi distance origin)
+        // Rotary position of the query: its own (cache_seqlens + i) when causal
+        // or windowed, else cache_seqlens for every row.
+        const int rpos = sq.L0 + (a.causal || a.local_window ? qpos : 0);
         f16x8 qB[HD / 16];
         {
             const f16 *qp = (const f16 *)a.q.ptr + int64_t(b) * a.q.batch_stride + int64_t(qpos) * a.q.row_stride +
@@ -221,6 +270,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
     #pragma unroll
             for (int g = 0; g < HD / 16; ++g) {
                 u32x4 v = row_ok ? ldg16(qp + 16 * g + 8 * hh) : zero_u4();
+                if (EXT && row_ok && 16 * g + 8 * hh < a.rotary_dim) v = rotary8(a, v, qp, 16 * g + 8 * hh, rpos);
                 if (neg) v = neg_h8(v);
                 qB[g] = as_h8(v);
             }
@@ -542,6 +592,11 @@ static int check_kv(const fa_kvcache_args *p) {
     if (a.block_table && (a.page_block_size <= 0 || a.page_block_size % kTile != 0)) return FA_ERR_INVALID_ARG;
     if (a.block_table && a.cache_batch_idx) return FA_ERR_INVALID_ARG;
     if (!(a.softcap >= 0.f) || a.softcap == INFINITY) return FA_ERR_INVALID_ARG;  // NaN fails too
+    if (a.rotary_dim != 0 &&
+        (a.rotary_dim < 0 || a.rotary_dim % 16 != 0 || a.rotary_dim > a.head_dim || a.rotary_seqlen < 1 ||
+         !a.rotary_cos || !a.rotary_sin || !a.k_new.ptr ||
+         ((reinterpret_cast<uintptr_t>(a.rotary_cos) | reinterpret_cast<uintptr_t>(a.rotary_sin)) & 15u)))
+        return FA_ERR_INVALID_ARG;
     return FA_OK;
 }
 
@@ -622,7 +677,7 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     } else {
         run.batch_order = nullptr;  // natural order
     }
-    const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes;
+    const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
     auto go = [&](auto hd_tag, auto dyn_tag, auto ext_tag) {
         constexpr int HD = decltype(hd_tag)::value;
         constexpr bool DYN = decltype(dyn_tag)::value, EXT = decltype(ext_tag)::value;

@@ -46,7 +46,8 @@ inline bool is_aligned(const at::Tensor &t) {
     for (int64_t i = 0; ok && i + 1 < t.dim(); ++i) ok = (t.stride(i) % 8) == 0 || t.size(i) == 1;
     return ok;
 }
-inline at::Tensor aligned(const at::Tensor &t) { return is_aligned(t) ? t : t.contiguous(); }
+// A fresh contiguous copy when not (contiguous() alone would keep a misaligned base).
+inline at::Tensor aligned(const at::Tensor &t) { return is_aligned(t) ? t : t.clone(at::MemoryFormat::Contiguous); }
 
 // A gradient output: the caller's tensor (for instance one slice of a packed
 // dqkv) when it is given, written in place if its layout suits the kernels and
@@ -328,14 +329,10 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     // capacity and cache_batch_idx bounds are checked on the device instead of
     // by host reads (no synchronisation, so the call can be graph-captured):
     // 1 (capacity) / 2 (cache row) are ORed into it for the caller to report.
-    (void)rotary_interleaved;
-    TORCH_CHECK(!rotary_cos.has_value() && !rotary_sin.has_value(),
-                "Turing KV-cache does not support rotary embeddings yet");
-
     TORCH_CHECK(!out_opt.has_value(), "Turing KV-cache does not support a preallocated output tensor yet");
-    // Local windows, softcap, ALiBi and cache_leftpad (rejected by the
-    // reference, flash_api.cpp:530-539) take upstream FlashAttention's
-    // semantics; they run in the split kernel.
+    // Rotary embeddings, local windows, softcap, ALiBi and cache_leftpad
+    // (rejected by the reference, flash_api.cpp:530-539) take upstream
+    // FlashAttention's semantics; attention with them runs in the split kernel.
     TORCH_CHECK(std::isfinite(softcap), "softcap must be finite");
     TORCH_CHECK(num_splits >= 0, "num_splits must be non-negative");
 
@@ -501,7 +498,37 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
         a.alibi_slopes = al.data_ptr<float>();
         a.alibi_batch_stride = al.dim() == 2 ? al.stride(0) : 0;
     }
-    const bool options = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes;
+    at::Tensor cos_t, sin_t;
+    if (rotary_cos.has_value() || rotary_sin.has_value()) {
+        // Upstream's checks for the rotary tables.
+        TORCH_CHECK(has_k, "If rotary cos/sin are provided, new key / value to be appended to KV cache must also be provided");
+        TORCH_CHECK(rotary_cos.has_value() && rotary_sin.has_value(),
+                    "If rotary cos is provided, rotary sin must also be provided");
+        cos_t = *rotary_cos;
+        sin_t = *rotary_sin;
+        TORCH_CHECK(cos_t.is_cuda() && cos_t.device() == q.device() && sin_t.is_cuda() && sin_t.device() == q.device(),
+                    "rotary_cos / rotary_sin must be CUDA tensors on the device of q");
+        TORCH_CHECK(cos_t.scalar_type() == at::kHalf && sin_t.scalar_type() == at::kHalf,
+                    "rotary_cos / rotary_sin must have the same dtype as query");
+        TORCH_CHECK(cos_t.dim() == 2, "rotary_cos must have shape (seqlen_ro, rotary_dim / 2)");
+        const int64_t rotary_dim = 2 * cos_t.size(1), seqlen_ro = cos_t.size(0);
+        TORCH_CHECK(rotary_dim <= head_size, "rotary_dim must be <= headdim");
+        TORCH_CHECK(rotary_dim % 16 == 0, "Only rotary dimensions divisible by 16 are currently supported");
+        TORCH_CHECK(sin_t.dim() == 2 && sin_t.size(0) == seqlen_ro && sin_t.size(1) == rotary_dim / 2,
+                    "rotary_sin must have the shape of rotary_cos");
+        TORCH_CHECK(seqlen_ro >= 1 && seqlen_ro <= INT32_MAX, "rotary_cos must have at least one row");
+        if (has_block_table)
+            TORCH_CHECK(seqlen_ro >= seqlen_cache, "cos/sin seqlen must be at least the seqlen of KV cache");
+        cos_t = aligned(cos_t);
+        sin_t = aligned(sin_t);
+        a.rotary_cos = cos_t.data_ptr();
+        a.rotary_sin = sin_t.data_ptr();
+        a.rotary_dim = int32_t(rotary_dim);
+        a.rotary_seqlen = int32_t(seqlen_ro);
+        a.rotary_interleaved = rotary_interleaved ? 1 : 0;
+    }
+    const bool options =
+        a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
 
     check_rc(fa_kv_append(&a, stream), "fa_kv_append");
 

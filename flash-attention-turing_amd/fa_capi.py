@@ -65,6 +65,8 @@ class FaKvcacheArgs(ctypes.Structure):
         ("cache_capacity", _i32), ("cache_batch", _i32), ("status", _p),
         ("local_window", _i32), ("window_left", _i32), ("window_right", _i32), ("softcap", _f32),
         ("cache_leftpad", _p), ("alibi_slopes", _p), ("alibi_batch_stride", _i64),
+        ("rotary_cos", _p), ("rotary_sin", _p), ("rotary_dim", _i32), ("rotary_seqlen", _i32),
+        ("rotary_interleaved", _i32),
     ]
 
 
@@ -181,7 +183,8 @@ def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, caus
 def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: float, causal: bool, num_splits: int,
                  k_new=None, v_new=None, cache_batch_idx=None, block_table=None, out_accum=None,
                  lse_accum=None, batch_order=None, status=None, window=(-1, -1),
-                 softcap: float = 0.0, cache_leftpad=None, alibi_slopes=None) -> FaKvcacheArgs:
+                 softcap: float = 0.0, cache_leftpad=None, alibi_slopes=None, rotary_cos=None, rotary_sin=None,
+                 rotary_interleaved: bool = True) -> FaKvcacheArgs:
     a = FaKvcacheArgs()
     a.q, a.k_cache, a.v_cache, a.o = (tensor_desc(x) for x in (q, k_cache, v_cache, o))
     a.k_new, a.v_new = tensor_desc(k_new), tensor_desc(v_new)
@@ -206,4 +209,8 @@ def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: floa
     a.cache_leftpad = ptr(cache_leftpad)
     a.alibi_slopes = ptr(alibi_slopes)
     a.alibi_batch_stride = alibi_slopes.stride(0) if alibi_slopes is not None and alibi_slopes.dim() == 2 else 0
+    a.rotary_cos, a.rotary_sin = ptr(rotary_cos), ptr(rotary_sin)
+    a.rotary_dim = 0 if rotary_cos is None else 2 * rotary_cos.shape[1]
+    a.rotary_seqlen = 0 if rotary_cos is None else rotary_cos.shape[0]
+    a.rotary_interleaved = int(rotary_interleaved)
     return a

@@ -92,16 +92,18 @@ def _flash_attn_kvcache_forward(
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale: float, causal: bool,
     num_splits: int, status: Optional[torch.Tensor] = None, window_size: Tuple[int, int] = (-1, -1),
     softcap: float = 0.0, cache_leftpad: Optional[torch.Tensor] = None, alibi_slopes: Optional[torch.Tensor] = None,
+    rotary_cos: Optional[torch.Tensor] = None, rotary_sin: Optional[torch.Tensor] = None,
+    rotary_interleaved: bool = True,
 ):
     tensors = (q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, cache_leftpad, alibi_slopes)
     q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, cache_leftpad, alibi_slopes = (
         maybe_contiguous(t) for t in tensors
     )
-    # The 20-argument binding of flash_api.cpp:508-528; rotary and a
-    # preallocated out are passed as "absent".
+    # The 20-argument binding of flash_api.cpp:508-528; a preallocated out is
+    # passed as "absent".
     out, lse = flash_attn_gpu.fwd_kvcache(
         q, k_cache, v_cache, k, v, cache_seqlens,
-        None, None,            # rotary_cos, rotary_sin
+        rotary_cos, rotary_sin,
         cache_batch_idx,
         cache_leftpad,
         block_table,
@@ -110,7 +112,7 @@ def _flash_attn_kvcache_forward(
         softmax_scale, causal,
         int(window_size[0]), int(window_size[1]),
         float(softcap),
-        True,                  # rotary_interleaved
+        bool(rotary_interleaved),
         num_splits,
         status,                # device-side input checks instead of host reads, when given
     )
@@ -329,11 +331,11 @@ def flash_attn_varlen_kvpacked_func(
 
 
 def _validate_unsupported_kvcache_args(rotary_cos, rotary_sin, cache_leftpad, window_size, softcap, alibi_slopes):
-    # interface.py:617-634 rejects all five; local windows, softcap, ALiBi and
-    # cache_leftpad are supported here (upstream FlashAttention's semantics),
-    # rotary embeddings are not.
-    if rotary_cos is not None or rotary_sin is not None:
-        raise NotImplementedError("Turing KV-cache does not support rotary embeddings yet")
+    # interface.py:617-634 rejects all five; here they are supported with
+    # upstream FlashAttention's semantics, so only their types are checked.
+    for name, t in (("rotary_cos", rotary_cos), ("rotary_sin", rotary_sin)):
+        if t is not None and (not isinstance(t, torch.Tensor) or t.dtype != torch.float16 or t.dim() != 2):
+            raise TypeError(f"{name} must be a 2-D torch.float16 tensor (seqlen_ro, rotary_dim / 2)")
     if len(tuple(window_size)) != 2 or not all(isinstance(w, int) for w in window_size):
         raise TypeError("window_size must be a pair of ints")
     if not math.isfinite(softcap):
@@ -429,14 +431,19 @@ def flash_attn_with_kvcache(
 
     Supports contiguous caches (optionally remapped by cache_batch_idx), paged
     caches via block_table, in-place append of k/v at cache_seqlens and split-KV
-    (num_splits, 0 = heuristic).  Rotary embeddings raise NotImplementedError,
-    as in the reference.  Beyond the reference (which rejects them),
-    window_size, softcap, alibi_slopes and cache_leftpad work with upstream
-    FlashAttention's semantics: query i, at key position p = i + L - seqlen_q,
-    sees keys [p - left, p + right] (-1: unbounded; causal caps the right side
-    at p); softcap > 0 replaces each scaled score x by softcap * tanh(x / softcap);
-    ALiBi (fp32 slopes [nheads] or [batch, nheads]) adds -slope * |p - j| to the
-    score of key j; keys before cache_leftpad[b] (int32 [batch]) do not exist.
+    (num_splits, 0 = heuristic).  Beyond the reference (which rejects them),
+    rotary embeddings, window_size, softcap, alibi_slopes and cache_leftpad work
+    with upstream FlashAttention's semantics: query i, at key position
+    p = i + L - seqlen_q, sees keys [p - left, p + right] (-1: unbounded; causal
+    caps the right side at p); softcap > 0 replaces each scaled score x by
+    softcap * tanh(x / softcap); ALiBi (fp32 slopes [nheads] or [batch, nheads])
+    adds -slope * |p - j| to the score of key j; keys before cache_leftpad[b]
+    (int32 [batch]) do not exist.  With rotary_cos / rotary_sin (fp16
+    [seqlen_ro, rotary_dim / 2]; k and v required), the first rotary_dim channels
+    of new key t are rotated at position cache_seqlens[b] + t before the append,
+    and q's at cache_seqlens[b] + i when causal or windowed, else at
+    cache_seqlens[b]; rotary_interleaved pairs channels (2j, 2j + 1), otherwise
+    (j, j + rotary_dim / 2).
 
     validate (after the reference's arguments): True checks the cache capacity
     and cache_batch_idx on the host, raising at once as the reference does (two
@@ -510,6 +517,6 @@ def flash_attn_with_kvcache(
     status = None if validate else _kv_status(q.device)
     out, lse = _flash_attn_kvcache_forward(
         q, k_cache, v_cache, k, v, cache_seqlens, cache_batch_idx, block_table, softmax_scale, causal, num_splits,
-        status, tuple(window_size), softcap, cache_leftpad, alibi_slopes,
+        status, tuple(window_size), softcap, cache_leftpad, alibi_slopes, rotary_cos, rotary_sin, rotary_interleaved,
     )
     return (out, lse) if return_softmax_lse else out

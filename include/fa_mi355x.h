@@ -152,6 +152,19 @@ typedef struct fa_kvcache_args {
     const int32_t *cache_leftpad;   /* [batch] first valid key of each sequence, or NULL            */
     const float *alibi_slopes;      /* fp32 [nheads] (batch stride 0) or [batch][nheads], or NULL   */
     int64_t alibi_batch_stride;
+    /* Rotary embedding on append (upstream FlashAttention's, also rejected by the
+     * reference): with rotary_dim > 0 (a multiple of 16, at most head_dim; k_new
+     * required), channels [0, rotary_dim) of appended key t of sequence b are
+     * rotated at position cache_seqlens[b] + t before the store, and those of
+     * query row i at cache_seqlens[b] + i when causal or local_window, else at
+     * cache_seqlens[b]; position p's angles are row p of rotary_cos / rotary_sin
+     * (fp16 [rotary_seqlen][rotary_dim / 2], contiguous, 16-byte aligned; a
+     * position past the last row takes the last row).  Interleaved rotates
+     * channel pairs (2j, 2j + 1) by angle j, otherwise (j, j + rotary_dim / 2). */
+    const void *rotary_cos, *rotary_sin;
+    int32_t rotary_dim;             /* 0: no rotary embedding                                       */
+    int32_t rotary_seqlen;
+    int32_t rotary_interleaved;
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);

@@ -14,6 +14,16 @@ means right = 0), softcap c > 0 replaces the scaled score s * scale by
 c * tanh(s * scale / c), ALiBi adds -slope_h * |i + L - sq - j| to the score
 fed to the softmax (slopes [h] or [b, h]), and cache_leftpad[b] is the first
 valid key of sequence b (positions unchanged).
+
+Rotary embeddings (``rotary_embed``) restate upstream FlashAttention's
+rotary form (flash_attn/layers/rotary.py, apply_rotary_emb_torch, v2.x;
+the reference's signature takes rotary_cos / rotary_sin and rejects them):
+with rotary_dim = 2 * cos.shape[1], channel pairs (j, j + rotary_dim / 2)
+(or (2j, 2j + 1) interleaved) are rotated by the angle whose cosine and sine
+are cos[p, j], sin[p, j] at the row's position p; channels past rotary_dim are
+kept.  Appended key t of sequence b sits at position cache_seqlens[b] + t, and
+query i at cache_seqlens[b] + i when causal or windowed, else at
+cache_seqlens[b].
 """
 
 from typing import List, Optional, Tuple
@@ -66,6 +76,49 @@ def append_paged(
             blk = table[bi][pos // page]
             k_cache[blk, pos % page] = k[bi, t]
             v_cache[blk, pos % page] = v[bi, t]
+
+
+def rotary_embed(
+    x: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: torch.Tensor,
+    interleaved: bool,
+    compute: torch.dtype = torch.float32,
+    out_dtype: Optional[torch.dtype] = None,
+) -> torch.Tensor:
+    """Rotate the first 2 * cos.shape[1] channels of x [b, s, h, d] at
+    positions [b, s] (row p of cos / sin [seqlen_ro, rotary_dim / 2]).
+
+    compute float32 on fp16 inputs: each product is exact, so every output is
+    the exact rotation rounded once to fp32, then to ``out_dtype`` (x's dtype
+    by default).  A position past the table takes its last row (this package's
+    choice; upstream reads past the table there)."""
+    rd = 2 * cos.shape[1]
+    half = rd // 2
+    pos = positions.long().clamp(0, cos.shape[0] - 1)
+    c = cos.to(compute)[pos][:, :, None, :]  # b s 1 half
+    sn = sin.to(compute)[pos][:, :, None, :]
+    xr = x[..., :rd].to(compute)
+    if interleaved:
+        a, bb = xr[..., 0::2], xr[..., 1::2]
+    else:
+        a, bb = xr[..., :half], xr[..., half:]
+    ra = a * c - bb * sn
+    rb = a * sn + bb * c
+    if interleaved:
+        rot = torch.stack((ra, rb), dim=-1).flatten(-2)
+    else:
+        rot = torch.cat((ra, rb), dim=-1)
+    out = x.to(compute).clone()
+    out[..., :rd] = rot
+    return out.to(out_dtype or x.dtype)
+
+
+def rotary_positions(cache_seqlens: torch.Tensor, n: int, per_row: bool) -> torch.Tensor:
+    """[b, n] positions: cache_seqlens[b] + i (per_row) or cache_seqlens[b]."""
+    step = torch.arange(n)[None, :] if per_row else torch.zeros((1, n), dtype=torch.int64)
+    return cache_seqlens.long()[:, None] + step
 
 
 def materialize(

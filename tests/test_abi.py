@@ -157,3 +157,18 @@ def test_validation_errors_before_any_launch(lib):
     assert ws(ctypes.byref(kv)) == 3 * 2 * 4 * 1 * (128 + 1) * 4
     kv.num_splits = 1
     assert ws(ctypes.byref(kv)) == 0
+    # Rotary: rotary_dim a multiple of 16 up to head_dim, both aligned tables,
+    # at least one row, and new keys to rotate.
+    kv.block_table, kv.page_block_size, kv.cache_batch_idx = None, 0, None
+    kv.rotary_cos = kv.rotary_sin = P
+    kv.rotary_dim, kv.rotary_seqlen = 64, 16
+    assert split(ctypes.byref(kv), None) == -1  # no k_new
+    kv.k_new = kv.v_new = tensor()
+    kv.rotary_dim = 40
+    assert split(ctypes.byref(kv), None) == -1  # not a multiple of 16
+    kv.rotary_dim = 144
+    assert split(ctypes.byref(kv), None) == -1  # wider than head_dim
+    kv.rotary_dim, kv.rotary_sin = 64, P + 8
+    assert split(ctypes.byref(kv), None) == -1  # misaligned sin table
+    kv.rotary_sin, kv.rotary_seqlen = P, 0
+    assert split(ctypes.byref(kv), None) == -1  # empty table

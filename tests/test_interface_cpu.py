@@ -91,20 +91,18 @@ def test_rejects_capacity_overrun():
         )
 
 
-@pytest.mark.parametrize(
-    "kwargs,msg",
-    [
-        (dict(rotary_cos=_t(8, 32), rotary_sin=_t(8, 32)), "rotary embeddings"),
-    ],
-)
-def test_explicit_feature_rejections_come_first(kwargs, msg):
-    # head_dim 96 and unpaired k would also be errors: the feature check wins.
-    with pytest.raises(NotImplementedError, match=msg):
-        fai.flash_attn_with_kvcache(_t(1, 2, 4, 96), _t(1, 8, 2, 96), _t(1, 8, 2, 96), k=_t(1, 1, 2, 96), **kwargs)
+def test_feature_type_checks_come_first():
+    # head_dim 96 and unpaired k would also be errors: the feature's own type
+    # check wins, as the reference's feature rejections did (interface.py:807-812).
+    with pytest.raises(TypeError, match="rotary_cos must be a 2-D torch.float16 tensor"):
+        fai.flash_attn_with_kvcache(_t(1, 2, 4, 96), _t(1, 8, 2, 96), _t(1, 8, 2, 96), k=_t(1, 1, 2, 96),
+                                    rotary_cos=_t(8, 32), rotary_sin=_t(8, 32))
 
 
 @pytest.mark.parametrize("kwargs", [dict(window_size=(4, 0)), dict(softcap=30.0), dict(window_size=(-1, 2), softcap=5),
-                                    dict(alibi_slopes=_t(4)), dict(cache_leftpad=torch.zeros(1, dtype=torch.int32))])
+                                    dict(alibi_slopes=_t(4)), dict(cache_leftpad=torch.zeros(1, dtype=torch.int32)),
+                                    dict(rotary_cos=_t(8, 16, dtype=torch.float16), rotary_sin=_t(8, 16, dtype=torch.float16),
+                                         rotary_interleaved=False)])
 def test_window_and_softcap_are_accepted(kwargs):
     # The reference rejects these (interface.py:617-634); here they pass the
     # Python checks (upstream FlashAttention's semantics) and reach the next

@@ -1,7 +1,8 @@
-"""Local windows, softcap, ALiBi and cache_leftpad in flash_attn_with_kvcache
-(upstream FlashAttention semantics; the reference's signature takes these but
-rejects them, flash_attention_interface.py:617-634) against the extended CPU
-oracle.
+"""Local windows, softcap, ALiBi, cache_leftpad and rotary embeddings in
+flash_attn_with_kvcache (upstream FlashAttention semantics; the reference's
+signature takes these but rejects them, flash_attention_interface.py:617-634)
+against the extended CPU oracle.  Rotated keys land in the cache bit for bit
+as the oracle rotates them.
 
 Bound: as for the other KV-cache outputs (the kernels are fp32 until the final
 fp16 rounding), 2x the error of the fp16-rounded oracle; LSE to fp32 precision.
@@ -54,8 +55,44 @@ def test_kvcache_alibi_leftpad(device, b, sq, h, hk, hd, cap, new, causal, split
     _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad)
 
 
-def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad):
-    g = torch.Generator().manual_seed(8000 + b * 13 + sq + hd + cap // 256 + (alibi is not None) + 2 * leftpad)
+CASES_ROTARY = [
+    # b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, rotary_dim, interleaved, leftpad
+    (3, 1, 8, 2, 128, 1024, 1, True, 0, True, False, (-1, -1), 128, False, False),
+    (3, 1, 8, 2, 128, 1024, 1, True, 4, False, True, (-1, -1), 64, True, False),
+    (2, 4, 8, 8, 64, 512, 4, True, 1, False, False, (-1, -1), 64, False, False),
+    (2, 4, 8, 8, 64, 512, 4, False, 2, True, False, (-1, -1), 32, True, False),
+    (2, 3, 6, 2, 64, 512, 2, False, 0, False, True, (40, 7), 48, False, True),
+    (2, 5, 4, 1, 128, 768, 5, True, 3, True, False, (-1, -1), 80, True, True),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,sq,h,hk,hd,cap,new,causal,splits,paged,remap,window,rotary_dim,interleaved,leftpad",
+                         CASES_ROTARY)
+def test_kvcache_rotary(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, rotary_dim,
+                        interleaved, leftpad):
+    _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, 0.0, None, leftpad,
+           rotary=(rotary_dim, interleaved))
+
+
+@pytest.mark.gpu
+def test_kvcache_rotary_needs_new_keys(device):
+    q = torch.zeros((1, 1, 4, 64), dtype=torch.float16, device=device)
+    kc = torch.zeros((1, 256, 1, 64), dtype=torch.float16, device=device)
+    tab = torch.zeros((256, 16), dtype=torch.float16, device=device)
+    with pytest.raises(RuntimeError, match="new key / value to be appended"):
+        fai.flash_attn_with_kvcache(q, kc, kc.clone(), rotary_cos=tab, rotary_sin=tab,
+                                    cache_seqlens=torch.ones(1, dtype=torch.int32, device=device))
+    k = torch.zeros((1, 1, 1, 64), dtype=torch.float16, device=device)
+    with pytest.raises(RuntimeError, match="divisible by 16"):
+        fai.flash_attn_with_kvcache(q, kc, kc.clone(), k, k, rotary_cos=tab[:, :12], rotary_sin=tab[:, :12],
+                                    cache_seqlens=torch.ones(1, dtype=torch.int32, device=device))
+
+
+def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad,
+           rotary=None):
+    g = torch.Generator().manual_seed(8000 + b * 13 + sq + hd + cap // 256 + (alibi is not None) + 2 * leftpad
+                                      + (0 if rotary is None else rotary[0]))
     rows = b + 2 if remap else b
     kc = randn16((rows, cap, hk, hd), g)
     vc = randn16((rows, cap, hk, hd), g)
@@ -71,6 +108,10 @@ def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, win
     elif alibi == "bh":
         slopes = torch.rand((b, h), generator=g) * 0.5
     lpad = torch.randint(0, 64, (b,), generator=g, dtype=torch.int32) if leftpad else None
+    cos = sin = None
+    if rotary is not None:
+        ang = torch.rand((cap, rotary[0] // 2), generator=g, dtype=torch.float64) * 2 * torch.pi
+        cos, sin = torch.cos(ang).to(torch.float16), torch.sin(ang).to(torch.float16)
     table = None
     kcp, vcp = kc, vc
     if paged:
@@ -90,10 +131,17 @@ def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, win
         window_size=window, softcap=softcap, return_softmax_lse=True,
         alibi_slopes=None if slopes is None else slopes.to(device),
         cache_leftpad=None if lpad is None else lpad.to(device),
+        rotary_cos=None if cos is None else cos.to(device), rotary_sin=None if sin is None else sin.to(device),
+        rotary_interleaved=True if rotary is None else rotary[1],
     )
     torch.cuda.synchronize()
     # Oracle: append, materialise the logical caches, attend.
     kr, vr = kcp.clone(), vcp.clone()
+    # Upstream's normalisation of bounds at least the capacity.
+    w = tuple(-1 if x >= cap else x for x in window)
+    if rotary is not None:
+        k = okv.rotary_embed(k, cos, sin, okv.rotary_positions(seqlens, new, True), rotary[1])
+        q = okv.rotary_embed(q, cos, sin, okv.rotary_positions(seqlens, sq, causal or w != (-1, -1)), rotary[1])
     if k is not None:
         if table is None:
             okv.append_contiguous(kr, vr, k, v, seqlens, batch_idx)
@@ -102,8 +150,6 @@ def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, win
     assert torch.equal(kcd.cpu(), kr) and torch.equal(vcd.cpu(), vr), "append differs from the oracle"
     ends = seqlens + new
     ku, vu = okv.materialize(kr, vr, ends, batch_idx, table)
-    # Upstream's normalisation of bounds at least the capacity.
-    w = tuple(-1 if x >= cap else x for x in window)
     o_ref, l_ref = okv.splitkv_attention(q, ku, vu, ends, hd ** -0.5, causal, max(splits, 1), window=w,
                                          softcap=softcap, alibi_slopes=slopes, leftpad=lpad)
     assert_2x("out", out.cpu(), o_ref, o_ref.to(torch.float16))

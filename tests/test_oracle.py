@@ -350,6 +350,84 @@ def test_splitkv_alibi_and_leftpad_known_answers():
         assert torch.allclose(o1[bi], bo[0], atol=1e-12) and torch.allclose(l1[bi], bl[0], atol=1e-12)
 
 
+def _rope_tables(seqlen, rd, dtype=D64, base=10000.0):
+    # cos / sin of the angles p * base^(-2j / rd), the usual rotary schedule.
+    inv = base ** (-torch.arange(0, rd, 2, dtype=D64) / rd)
+    ang = torch.arange(seqlen, dtype=D64)[:, None] * inv[None, :]
+    return torch.cos(ang).to(dtype), torch.sin(ang).to(dtype)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rotary_special_angles_and_tail(interleaved):
+    x = _rand((2, 3, 2, 64), 60, torch.float16)
+    rd, half = 32, 16
+    pos = torch.zeros((2, 3), dtype=torch.long)
+    one, zero = torch.ones((1, half), dtype=torch.float16), torch.zeros((1, half), dtype=torch.float16)
+    # Angle 0: identity, bit for bit.
+    assert torch.equal(okv.rotary_embed(x, one, zero, pos, interleaved), x)
+    # Quarter turn (cos 0, sin 1): (a, b) -> (-b, a) exactly; the tail is kept.
+    y = okv.rotary_embed(x, zero, one, pos, interleaved)
+    if interleaved:
+        assert torch.equal(y[..., 0:rd:2], -x[..., 1:rd:2]) and torch.equal(y[..., 1:rd:2], x[..., 0:rd:2])
+    else:
+        assert torch.equal(y[..., :half], -x[..., half:rd]) and torch.equal(y[..., half:rd], x[..., :half])
+    assert torch.equal(y[..., rd:], x[..., rd:])
+
+
+def test_rotary_hand_computed_and_interleaving_is_a_channel_permutation():
+    x = torch.tensor([1.0, 2.0, 3.0, 4.0], dtype=D64).reshape(1, 1, 1, 4)
+    c = torch.tensor([[0.6, 0.0]], dtype=D64)
+    s = torch.tensor([[0.8, 1.0]], dtype=D64)
+    pos = torch.zeros((1, 1), dtype=torch.long)
+    y = okv.rotary_embed(x, c, s, pos, False, compute=D64).flatten().tolist()
+    assert y == pytest.approx([1 * 0.6 - 3 * 0.8, 2 * 0.0 - 4 * 1.0, 1 * 0.8 + 3 * 0.6, 2 * 1.0 + 4 * 0.0], abs=1e-15)
+    y = okv.rotary_embed(x, c, s, pos, True, compute=D64).flatten().tolist()
+    assert y == pytest.approx([1 * 0.6 - 2 * 0.8, 1 * 0.8 + 2 * 0.6, 3 * 0.0 - 4 * 1.0, 3 * 1.0 + 4 * 0.0], abs=1e-15)
+    # The interleaved form is the half-split form on channels reordered
+    # (0, 2, 4, ..., 1, 3, 5, ...), bit for bit at fp16.
+    xx = _rand((2, 5, 3, 64), 61, torch.float16)
+    cos, sin = _rope_tables(40, 48, torch.float16)
+    pos = torch.randint(0, 40, (2, 5), generator=torch.Generator().manual_seed(62))
+    perm = torch.cat((torch.arange(0, 48, 2), torch.arange(1, 48, 2), torch.arange(48, 64)))
+    inv = torch.argsort(perm)
+    a = okv.rotary_embed(xx, cos, sin, pos, True)
+    b = okv.rotary_embed(xx[..., perm], cos, sin, pos, False)[..., inv]
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rotary_scores_depend_on_relative_position_only(interleaved):
+    # The defining property of rotary embeddings: <R(p) q, R(p') k> depends on
+    # p - p' only, and each rotated pair keeps its length.  A wrong pairing,
+    # sign or position index breaks it.
+    cos, sin = _rope_tables(64, 32)
+    q, k = _rand((1, 1, 1, 48), 63), _rand((1, 1, 1, 48), 64)
+
+    def score(p, pk):
+        qq = okv.rotary_embed(q, cos, sin, torch.tensor([[p]]), interleaved, compute=D64)
+        kk = okv.rotary_embed(k, cos, sin, torch.tensor([[pk]]), interleaved, compute=D64)
+        return float((qq * kk).sum())
+
+    for p, pk in ((7, 3), (20, 20), (5, 30)):
+        assert score(p, pk) == pytest.approx(score(p + 17, pk + 17), abs=1e-12)
+        assert score(p, pk) == pytest.approx(score(p + 33, pk + 33), abs=1e-12)
+    assert abs(score(7, 3) - score(8, 3)) > 1e-3  # it does depend on the offset
+    r = okv.rotary_embed(q, cos, sin, torch.tensor([[11]]), interleaved, compute=D64)
+    assert float((r * r).sum()) == pytest.approx(float((q * q).sum()), abs=1e-12)
+
+
+def test_rotary_positions():
+    seq = torch.tensor([5, 0, 9], dtype=torch.int32)
+    assert okv.rotary_positions(seq, 3, True).tolist() == [[5, 6, 7], [0, 1, 2], [9, 10, 11]]
+    assert okv.rotary_positions(seq, 2, False).tolist() == [[5, 5], [0, 0], [9, 9]]
+    # Past the table: the last row.
+    cos, sin = _rope_tables(8, 16, torch.float16)
+    x = _rand((1, 2, 1, 16), 65, torch.float16)
+    far = okv.rotary_embed(x, cos, sin, torch.tensor([[7, 30]]), False)
+    last = okv.rotary_embed(x, cos, sin, torch.tensor([[7, 7]]), False)
+    assert torch.equal(far, last)
+
+
 # --------------------------------------------------------------------------- twin
 
 
