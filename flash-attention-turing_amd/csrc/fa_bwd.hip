@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 #pragma unroll
         for (int t = 0; t < 8; ++t) dpart += float(ov[t]) * float(doB[g][t]);
     }
-    const float dsum = dpart + __shfl_xor(dpart, 32);
+    const float dsum = sum_xor32(dpart);
     const float lse2 = qv ? a.lse[lrow + qi] * kLog2e : 0.f;
     if (qv && hh == 0) {
         a.dsum[lrow + qi] = -dsum;  // -D: the dK/dV kernel seeds its dP accumulators with it

@@ -55,6 +55,20 @@ __device__ __forceinline__ int acc_lrow(int r, int h) { return 16 * (r >> 3) + 8
 // Natural row of accumulator r in lane half h (no permutation at load).
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
+// Maximum / sum of x over lanes l and l ^ 32, in every lane.  v_permlane32_swap
+// of x with itself leaves x[l % 32] in one result and x[l % 32 + 32] in the
+// other, so this is one VALU op instead of an LDS round trip (ds_bpermute);
+// both halves compute lo + hi in the same order, so the sum is the same bits
+// in all lanes.
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
 

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(co
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_xor32(mx);
         const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
         if (__builtin_amdgcn_ballot_w64(mx_t > m_t + kRescaleSlack) != 0) {
             const float m_new = fmaxf(m_t, mx_t);
@@ -235,8 +235,8 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(co
     for (int nb = n_full; nb < n_blocks; ++nb) block(nb, std::true_type{});
 
     // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
-    const float l_tot = l_p + __shfl_xor(l_p, 32);
-    const float lo_tot = l_o + __shfl_xor(l_o, 32);
+    const float l_tot = sum_xor32(l_p);
+    const float lo_tot = sum_xor32(l_o);
     if (qi < sq) {
         const float inv = lo_tot > 0.f ? 1.f / lo_tot : 0.f;
         f16 *orow = op + int64_t(qi) * ors;

@@ -376,7 +376,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
                 if (key < s0 || key >= s1 || key > lim || (EXT && key < w_lo)) s[r] = -INFINITY;
                 mx = fmaxf(mx, s[r]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = max_xor32(mx);
             const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
             const float m_new = fmaxf(m_t, mx_t);
             const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
             run(std::false_type{});
 
         // Merge the four waves: each publishes (m, l) per row and its O^T tile.
-        const float l_w = l_p + __shfl_xor(l_p, 32);
+        const float l_w = sum_xor32(l_p);
         float *mrow = reinterpret_cast<float *>(smem + kKvWaves * C::WAVE_LDS);
         float *lrow = mrow + kKvWaves * 32;
         __syncthreads();  // every wave is done with its ring
