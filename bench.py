@@ -26,6 +26,7 @@ Prints ONE JSON line.
 """
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -230,6 +231,9 @@ def varlen_setup(device, seed=2):
     scale = d ** -0.5
     fa = fa_capi.fwd_args(q, k, v, o, lse, scale, True, cu_d, cu_d, mx, mx)
     ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, True, cu_d, cu_d, mx, mx)
+    # The dK/dV work items in longest-first order (built on the device by fa_bwd_dkdv).
+    order = torch.empty(max(1, fa_capi.load().fa_bwd_order_len(ctypes.byref(ba))), dtype=torch.int32, device=device)
+    ba.work_order = order.data_ptr()
     launches = [
         ("fwd", lambda: fa_capi.call("fa_fwd", fa)),
         ("bwd_dq", lambda: fa_capi.call("fa_bwd_dq", ba)),
@@ -237,7 +241,7 @@ def varlen_setup(device, seed=2):
     ]
     unit = h * d * sum(int(n) * (int(n) + 1) // 2 for n in lens)
     info = {"sequences": 16, "total_tokens": total, "max_seqlen": mx, "heads": h, "heads_k": hk, "head_dim": d}
-    return launches, info, unit, dict(o=o, dq=dq, dk=dk, dv=dv)
+    return launches, info, unit, dict(o=o, dq=dq, dk=dk, dv=dv, order=order)
 
 
 def longctx_setup(device, seed=4):

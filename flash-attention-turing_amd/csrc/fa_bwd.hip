@@ -241,8 +241,60 @@ struct DkvCfg {
     static_assert(XCH <= LDS, "partial-sum exchange reuses the tiles' LDS");
 };
 
+// Varlen dK/dV work order.  Item it = b * nnb + nb is key block nb of
+// sequence b; its work is the number of query rows that see the block
+// (causal: min(sq, sk - 128 nb), else sq).  One workgroup counting-sorts the
+// items by that number in 64-row buckets, largest first (a histogram, a scan
+// over the buckets in descending order, then a scatter through per-bucket
+// cursors), and fills the rest of the list with -1 (no key in the block), so
+// the dK/dV grid starts the longest items first and its empty workgroups come
+// last.  Order within a bucket follows the LDS atomics; every item's result is
+// independent of it.
+constexpr int kOrderThreads = 1024, kOrderBuckets = 1024;
+
+__global__ __launch_bounds__(kOrderThreads) void bwd_order_kernel(const fa_bwd_args a, const int nnb) {
+    __shared__ int hist[kOrderBuckets];
+    __shared__ int scan[kOrderBuckets];
+    const int tid = threadIdx.x;
+    const int n_items = a.batch * nnb;
+    auto bucket = [&](int it) {
+        const int b = it / nnb, nb = it - b * nnb;
+        const int sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
+        const int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.seqlen_q;
+        const int k0 = nb * 128;
+        if (k0 >= sk) return -1;
+        const int rows = a.causal ? max(0, min(sq, sk - k0)) : max(sq, 0);
+        return min(rows >> 6, kOrderBuckets - 1);
+    };
+    hist[tid] = 0;
+    __syncthreads();
+    for (int it = tid; it < n_items; it += kOrderThreads) {
+        const int k = bucket(it);
+        if (k >= 0) atomicAdd(&hist[k], 1);
+    }
+    __syncthreads();
+    // Inclusive scan of the counts in descending bucket order (slot t = bucket 1023 - t).
+    const int c = hist[kOrderBuckets - 1 - tid];
+    scan[tid] = c;
+    __syncthreads();
+    for (int d = 1; d < kOrderBuckets; d <<= 1) {
+        const int v = tid >= d ? scan[tid - d] : 0;
+        __syncthreads();
+        scan[tid] += v;
+        __syncthreads();
+    }
+    hist[kOrderBuckets - 1 - tid] = scan[tid] - c;  // first slot of the bucket
+    const int total = scan[kOrderBuckets - 1];
+    __syncthreads();
+    for (int it = tid; it < n_items; it += kOrderThreads) {
+        const int k = bucket(it);
+        if (k >= 0) a.work_order[atomicAdd(&hist[k], 1)] = it;
+    }
+    for (int i = total + tid; i < n_items; i += kOrderThreads) a.work_order[i] = -1;
+}
+
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_args a) {
+__global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_args a, const int nnb) {
     using C = DkvCfg<HD>;
     constexpr int BN = C::BN, BM = C::BM, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[C::LDS];
@@ -251,10 +303,21 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int kg = wave & 3, half = wave >> 2;                  // key group, query half
     const int col = lane & 31, hh = lane >> 5;
-    const int bh_count = a.batch * a.nheads_k;
-    const int bhk = blockIdx.x % bh_count;
-    const int nb = blockIdx.x / bh_count;  // smallest key blocks (most queries) first
-    const int b = bhk / a.nheads_k, hk = bhk - b * a.nheads_k;
+    int b, hk, nb;
+    if (a.work_order && a.cu_seqlens_k) {
+        // Item of the device-built order (kv head fastest); -1: no keys.
+        const int it = a.work_order[blockIdx.x / a.nheads_k];
+        if (it < 0) return;
+        b = __builtin_amdgcn_readfirstlane(it / nnb);
+        nb = __builtin_amdgcn_readfirstlane(it - b * nnb);
+        hk = blockIdx.x % a.nheads_k;
+    } else {
+        const int bh_count = a.batch * a.nheads_k;
+        const int bhk = blockIdx.x % bh_count;
+        nb = blockIdx.x / bh_count;  // smallest key blocks (most queries) first
+        b = bhk / a.nheads_k;
+        hk = bhk - b * a.nheads_k;
+    }
     const int G = a.nheads / a.nheads_k;
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
     const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
@@ -557,10 +620,17 @@ static int launch_dq(const fa_bwd_args &a, hipStream_t s) {
 template <int HD, bool CAUSAL>
 static int launch_dkdv(const fa_bwd_args &a, hipStream_t s) {
     // seqlen_k bounds every sequence's key count (max_seqlen_k for varlen).
+    static_assert(DkvCfg<HD>::BN == 128, "bwd_order_kernel and fa_bwd_order_len assume 128-key blocks");
     const int nnb = (a.seqlen_k + DkvCfg<HD>::BN - 1) / DkvCfg<HD>::BN;
     const int64_t grid = int64_t(nnb) * a.batch * a.nheads_k;
     if (grid == 0) return FA_OK;
-    hipLaunchKernelGGL((bwd_dkdv_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kDkvThreads), 0, s, a);
+    if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+    if (a.work_order && a.cu_seqlens_k) {
+        hipLaunchKernelGGL(bwd_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, a, nnb);
+        const int rc = int(hipGetLastError());
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL((bwd_dkdv_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kDkvThreads), 0, s, a, nnb);
     return int(hipGetLastError());
 }
 
@@ -601,6 +671,11 @@ extern "C" int fa_bwd_dkdv(const fa_bwd_args *args, void *stream) {
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (a.head_dim == 128) return a.causal ? fa::launch_dkdv<128, true>(a, s) : fa::launch_dkdv<128, false>(a, s);
     return a.causal ? fa::launch_dkdv<64, true>(a, s) : fa::launch_dkdv<64, false>(a, s);
+}
+
+extern "C" size_t fa_bwd_order_len(const fa_bwd_args *a) {
+    if (!a || a->batch <= 0 || a->seqlen_k <= 0) return 0;
+    return size_t(a->batch) * size_t((a->seqlen_k + 127) / 128);
 }
 
 extern "C" int fa_bwd(const fa_bwd_args *args, void *stream) {

@@ -51,6 +51,7 @@ class FaBwdArgs(ctypes.Structure):
         ("lse", _p), ("dsum", _p), ("cu_seqlens_q", _p), ("cu_seqlens_k", _p),
         ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32), ("nheads", _i32), ("nheads_k", _i32),
         ("head_dim", _i32), ("lse_seqlen", _i32), ("softmax_scale", _f32), ("causal", _i32),
+        ("work_order", _p),
     ]
 
 
@@ -101,6 +102,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fa_kv_num_splits.restype = ctypes.c_int
     lib.fa_kv_workspace_bytes.argtypes = [ctypes.POINTER(FaKvcacheArgs)]
     lib.fa_kv_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_bwd_order_len.argtypes = [ctypes.POINTER(FaBwdArgs)]
+    lib.fa_bwd_order_len.restype = ctypes.c_size_t
     lib.fa_error_string.argtypes = [ctypes.c_int]
     lib.fa_error_string.restype = ctypes.c_char_p
     _lib = lib
@@ -158,7 +161,7 @@ def fwd_args(q, k, v, o, lse, softmax_scale: float, causal: bool, cu_seqlens_q=N
 
 
 def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, causal: bool, cu_seqlens_q=None,
-             cu_seqlens_k=None, max_seqlen_q: int = 0, max_seqlen_k: int = 0) -> FaBwdArgs:
+             cu_seqlens_k=None, max_seqlen_q: int = 0, max_seqlen_k: int = 0, work_order=None) -> FaBwdArgs:
     packed = cu_seqlens_q is not None
     a = FaBwdArgs()
     a.q, a.k, a.v, a.o, a.dout, a.dq, a.dk, a.dv = (
@@ -177,6 +180,7 @@ def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, caus
         a.lse_seqlen = q.shape[1]
     a.softmax_scale = softmax_scale
     a.causal = int(causal)
+    a.work_order = ptr(work_order)
     return a
 
 

@@ -90,8 +90,18 @@ typedef struct fa_bwd_args {
     int32_t lse_seqlen;
     float softmax_scale;
     int32_t causal;
+    /* Optional workspace for varlen calls (cu_seqlens_k set), fa_bwd_order_len(args)
+     * int32s: fa_bwd_dkdv (and fa_bwd) then first list the (sequence, key block)
+     * work items on the device, most query rows first, and launch the dK/dV
+     * workgroups in that order; NULL keeps the natural order, which is longest
+     * first only when every sequence has the same length.  Results are the same
+     * either way (each item is computed independently). */
+    int32_t *work_order;
 } fa_bwd_args;
 
+/* Length in int32s of the work_order workspace: batch * ceil(seqlen_k / 128).  No
+ * counterpart in the reference (its dK/dV grid is in natural order). */
+size_t fa_bwd_order_len(const fa_bwd_args *args);
 /* D = rowsum(dO * O) (flash_bwd_preprocess_kernel.h:23-96), stored negated in dsum plane 0. */
 int fa_bwd_preprocess(const fa_bwd_args *args, void *stream);
 /* dQ kernel (flash_bwd_kernel.h:25-609); computes and stores the dsum workspace itself. */

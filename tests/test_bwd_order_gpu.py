@@ -1,0 +1,82 @@
+"""Varlen dK/dV work order (the optional work_order workspace of fa_bwd_args).
+
+With the workspace, fa_bwd lists the (sequence, key block) items on the device,
+most query rows first, and launches the dK/dV workgroups in that order.  Every
+item is computed independently, so dQ, dK and dV must be bit-identical to the
+natural-order launch; the list itself must hold every item with keys exactly
+once, in non-increasing 64-row buckets of the rows that see the key block
+(causal: min(sq, sk - 128 nb), else sq), then -1 for the items with no keys.
+Cases: mixed lengths with empty and one-token sequences, sq != sk, GQA,
+head_dim 64 and 128, causal and not."""
+
+import ctypes
+
+import pytest
+import torch
+
+import fa_capi
+from helpers import cu_from_lengths, randn16
+
+CASES = [
+    # lengths_q, lengths_k, h, hk, hd, causal
+    ([1838, 2357, 653, 3709, 463, 1, 0, 552], None, 8, 2, 128, True),
+    ([200, 17, 90, 0, 700], [100, 300, 90, 5, 640], 6, 3, 128, False),
+    ([300, 17, 1000, 129], [129, 300, 1000, 17], 4, 1, 64, True),
+    ([64, 128, 256, 1000], None, 4, 4, 64, False),
+]
+
+
+def _bucket_rows(lq, lk, nb, causal):
+    k0 = 128 * nb
+    if k0 >= lk:
+        return None
+    rows = max(0, min(lq, lk - k0)) if causal else lq
+    return min(rows // 64, 1023)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens_q,lens_k,h,hk,hd,causal", CASES)
+def test_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, hd, causal):
+    lens_k = lens_k or lens_q
+    g = torch.Generator().manual_seed(6100 + sum(lens_q) + hd)
+    cu_q, cu_k = cu_from_lengths(lens_q), cu_from_lengths(lens_k)
+    tq, tk = int(cu_q[-1]), int(cu_k[-1])
+    mq, mk = max(lens_q), max(lens_k)
+    q, do = randn16((tq, h, hd), g).to(device), randn16((tq, h, hd), g).to(device)
+    k, v = randn16((tk, hk, hd), g).to(device), randn16((tk, hk, hd), g).to(device)
+    cq, ck = cu_q.to(device), cu_k.to(device)
+    o = torch.empty_like(q)
+    lse = torch.empty((len(lens_q), h, mq), dtype=torch.float32, device=device)
+    s = hd ** -0.5
+    fa = fa_capi.fwd_args(q, k, v, o, lse, s, causal, cq, ck, mq, mk)
+    fa_capi.call("fa_fwd", fa)  # raises on a non-zero code
+    grads = {}
+    for ordered in (False, True):
+        dq, dk, dv = torch.full_like(q, 7.0), torch.full_like(k, 7.0), torch.full_like(v, 7.0)
+        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=device)
+        ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, s, causal, cq, ck, mq, mk)
+        n = fa_capi.load().fa_bwd_order_len(ctypes.byref(ba))
+        nnb = (mk + 127) // 128
+        assert n == len(lens_q) * nnb
+        order = torch.full((n,), -7, dtype=torch.int32, device=device)
+        if ordered:
+            ba.work_order = order.data_ptr()
+        print(f"case lens_q={lens_q} hd={hd} causal={causal} ordered={ordered}", flush=True)
+        fa_capi.call("fa_bwd", ba)
+        torch.cuda.synchronize()
+        grads[ordered] = (dq.cpu(), dk.cpu(), dv.cpu())
+        if ordered:
+            got = order.cpu().tolist()
+            expect = {}
+            for b in range(len(lens_q)):
+                for nb in range(nnb):
+                    bk = _bucket_rows(lens_q[b], lens_k[b], nb, causal)
+                    if bk is not None:
+                        expect[b * nnb + nb] = bk
+            live = got[: len(expect)]
+            assert sorted(live) == sorted(expect), "the list must hold every item with keys once"
+            assert all(x == -1 for x in got[len(expect):]), "the rest of the list must be -1"
+            buckets = [expect[i] for i in live]
+            assert all(x >= y for x, y in zip(buckets, buckets[1:])), "items must come most rows first"
+    for a, b, name in zip(grads[False], grads[True], ("dq", "dk", "dv")):
+        assert torch.equal(a, b), f"{name} differs between the natural and the device-built order"
