@@ -251,6 +251,7 @@ struct DkvCfg {
 // last.  Order within a bucket follows the LDS atomics; every item's result is
 // independent of it.
 constexpr int kOrderThreads = 1024, kOrderBuckets = 1024;
+static_assert(kOrderThreads == kOrderBuckets, "one histogram bucket and one scan slot per thread");
 
 __global__ __launch_bounds__(kOrderThreads) void bwd_order_kernel(const fa_bwd_args a, const int nnb) {
     __shared__ int hist[kOrderBuckets];
