@@ -175,6 +175,12 @@ struct KvCfg {
     static constexpr int MAX_PAGES = 1024;              // page ids of one split staged in LDS
 };
 
+// The running maximum m that a row's probabilities P = exp2(S*c - m) are taken
+// against is raised (and O, l rescaled) only when some row of the wave finds a
+// score more than this many doublings above it; P stays below 2^8, and its hi +
+// lo fp16 halves still carry about 22 bits.
+constexpr float kKvRescaleSlack = 8.f;
+
 // tanh x = 1 - 2 / (e^(2x) + 1): exactly +-1 at the ends, an absolute error of a
 // few fp32 ulps of 1 in between (what a softcapped score needs).
 __device__ __forceinline__ float tanh_fast(float x) {
@@ -235,6 +241,18 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         // Keys whose tiles this item walks: the split, narrowed to the union of
         // its rows' windows.
         int k_lo = s0, k_hi = s1;
+        // Wave-uniform bounds of the keys every row of the tile sees: tiles in
+        // [max(s0, wlo_max), min(s1, lim_min + 1)) need no mask.
+        const int p_first = (rt * 32) / G + L - a.seqlen_q;  // smallest query position of the tile
+        int lim_min = a.causal ? p_first : L - 1;
+        int wlo_max = 0;
+        if constexpr (EXT) {
+            if (a.local_window) {
+                const int p_last = (min(R, rt * 32 + 32) - 1) / G + L - a.seqlen_q;
+                if (a.window_right >= 0) lim_min = min(lim_min, p_first + a.window_right);
+                if (a.window_left >= 0) wlo_max = p_last - a.window_left;
+            }
+        }
         if constexpr (EXT) {
             if (a.local_window) {
                 const int pos = qpos + L - a.seqlen_q;  // the query's own key position
@@ -370,26 +388,40 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
                 }
             }
             float mx = -INFINITY;
+            const bool interior = p0 >= s0 && p0 + kTile <= s1 && p0 + kTile - 1 <= lim_min && p0 >= wlo_max;
+            if (interior) {
     #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = p0 + acc_lrow(r, hh);
-                if (key < s0 || key >= s1 || key > lim || (EXT && key < w_lo)) s[r] = -INFINITY;
-                mx = fmaxf(mx, s[r]);
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            } else {
+    #pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = p0 + acc_lrow(r, hh);
+                    if (key < s0 || key >= s1 || key > lim || (EXT && key < w_lo)) s[r] = -INFINITY;
+                    mx = fmaxf(mx, s[r]);
+                }
             }
             mx = max_xor32(mx);
             const float mx_t = mx == -INFINITY ? -INFINITY : mx * cscale;
-            const float m_new = fmaxf(m_t, mx_t);
-            const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            if (__builtin_amdgcn_ballot_w64(mx_t > m_t + kKvRescaleSlack) != 0) {
+                const float m_new = fmaxf(m_t, mx_t);
+                const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
+                l_p *= alpha;
+    #pragma unroll
+                for (int dt = 0; dt < HD / 32; ++dt)
+    #pragma unroll
+                    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+                m_t = m_new;
+            }
+            const float m_use = m_t == -INFINITY ? 0.f : m_t;
+            // A masked score is -inf after every transform, and exp2(-inf) = 0.
             float rs = 0.f;
     #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = s[r] == -INFINITY ? 0.f : exp2_fast(fmaf(s[r], cscale, -m_use));
+                const float p = exp2_fast(fmaf(s[r], cscale, -m_use));
                 s[r] = p;
                 rs += p;
             }
-            l_p = l_p * alpha + rs;
-            m_t = m_new;
+            l_p += rs;
             // P stays fp32-accurate through the product: P = hi + lo with both halves fp16.
             f16x8 ph[2], pl[2];
     #pragma unroll
@@ -403,8 +435,6 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
                 }
     #pragma unroll
             for (int dt = 0; dt < HD / 32; ++dt) {
-    #pragma unroll
-                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     #pragma unroll
                 for (int gg = 0; gg < 2; ++gg) {
                     o[dt] = mfma32(va[dt][gg], ph[gg], o[dt]);
