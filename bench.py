@@ -49,10 +49,10 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 # (FETCH x 2.0, WRITE x 1.0); summary in profiles/hbm_bytes_pmc_c2_c4.md.
 # Re-measured whenever a kernel changes; None where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 6.609e8 + 6.816e7,
-    "bwd_dq": 6.007e8 + 7.353e7,
-    "bwd_dkdv": 7.438e8 + 1.512e8,
-    "kv_splitkv": 4.696e9 + 8.657e6,
+    "fwd": 7.989e8 + 6.816e7,
+    "bwd_dq": 6.386e8 + 7.353e7,
+    "bwd_dkdv": 7.886e8 + 1.500e8,
+    "kv_splitkv": 4.697e9 + 8.659e6,
 }
 
 
