@@ -93,3 +93,24 @@ def test_fwd_deterministic(device):
     a = fai.flash_attn_func(q, k, v, causal=True)
     b = fai.flash_attn_func(q, k, v, causal=True)
     assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_fwd_and_bwd_misaligned_base(device):
+    """Contiguous views whose base is not 16-byte aligned (an offset of one
+    element into a buffer) are copied to an aligned buffer by the host layer:
+    same bits as the aligned tensors, forward and backward."""
+    g = torch.Generator().manual_seed(13)
+    shape = (2, 130, 4, 64)
+    n = 2 * 130 * 4 * 64
+    bufs = [randn16((n + 1,), g).to(device) for _ in range(4)]
+    q, k, v, do = (b[1:].view(shape) for b in bufs)
+    assert q.is_contiguous() and q.data_ptr() % 16 != 0
+    qa, ka, va, doa = (t.clone() for t in (q, k, v, do))
+    out, lse = fai._flash_attn_forward(q, k, v, 0.125, True)
+    out_a, lse_a = fai._flash_attn_forward(qa, ka, va, 0.125, True)
+    assert torch.equal(out, out_a) and torch.equal(lse, lse_a)
+    grads = fai._flash_attn_backward(do, q, k, v, out, lse, 0.125, True)
+    grads_a = fai._flash_attn_backward(doa, qa, ka, va, out_a, lse_a, 0.125, True)
+    for x, y in zip(grads, grads_a):
+        assert torch.equal(x, y)
