@@ -21,6 +21,12 @@ CASES = [
     (hd, causal, sq, sk, HEADS[i % len(HEADS)], 1 + 2 * (i % 2), SCALES[i % len(SCALES)])
     for i, (hd, causal, (sq, sk)) in enumerate(itertools.product([64, 128], [False, True], SEQLENS))
 ]
+# More of the reference's (sq, sk) pairs (test_flash_attn.py:59-140), batch 1.
+EXTRA_SEQLENS = [(113, 203), (1, 1025), (1024, 1023), (897, 1025), (1536, 1536)]
+CASES += [
+    (128 if i % 2 == 0 else 64, i != 1, sq, sk, HEADS[i % len(HEADS)], 1, SCALES[i % len(SCALES)])
+    for i, (sq, sk) in enumerate(EXTRA_SEQLENS)
+]
 
 
 def _oracles(q, k, v, do, s, causal):

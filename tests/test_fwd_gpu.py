@@ -25,6 +25,14 @@ CASES = [
     (hd, causal, sq, sk, HEADS[i % len(HEADS)], 1 + 2 * (i % 2), SCALES[i % len(SCALES)])
     for i, (hd, causal, (sq, sk)) in enumerate(itertools.product([64, 128], [False, True], SEQLENS))
 ]
+# More of the reference's (sq, sk) pairs (test_flash_attn.py:59-140): ragged, sq = 1 against a long key
+# range, sq > sk, and 1k-2k squares; batch 1, so the CPU oracle stays fast.
+EXTRA_SEQLENS = [(113, 203), (108, 256), (256, 512), (1, 1025), (1024, 1023), (1023, 1024), (897, 1025),
+                 (2048, 2048)]
+CASES += [
+    (128 if i % 2 else 64, bool(i % 3), sq, sk, HEADS[i % len(HEADS)], 1, SCALES[i % len(SCALES)])
+    for i, (sq, sk) in enumerate(EXTRA_SEQLENS)
+]
 
 
 @pytest.mark.gpu
