@@ -376,9 +376,7 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     TileCopier<HD, BM, NT> qcp, ocp;
     qcp.init(qrs, wave, lane);
     ocp.init(dors, wave, lane);
-    // Copy (q-head, query block) j into stage st.  Rows past the sequence
-    // re-read its last row (finite values; their P and dS are zeroed below).
-    // Copies of the next block: running pointers to its first Q / dO row and
+    // Copies of the next (q-head, query block): running pointers to its first Q / dO row and
     // its LSE / D entries, advanced by one block per step (and moved to the
     // next q-head of the group after the last block of a head), so a step's
     // address work is a few scalar adds.  Rows past the sequence re-read its
@@ -518,12 +516,6 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     // block (masked).  Straight loops keep the dK/dV accumulators in place;
     // branching per block would copy them at every join.  Keys past the
     // sequence need no mask: their columns are never stored.
-    // Each wave walks the same sequence of blocks (one barrier per block) in
-    // four straight loops per q-head: blocks whose half sees none of its keys
-    // (skipped), diagonal blocks (masked), full blocks, and a ragged last
-    // block (masked).  Straight loops keep the dK/dV accumulators in place;
-    // branching per block would copy them at every join.  Keys past the
-    // sequence need no mask: their columns are never stored.
     int j = 0;  // running block index (stage j & 1)
     auto step = [&](int i, auto mask_tag, bool compute) {
         wait_vmem();
@@ -614,6 +606,7 @@ static int launch_dq(const fa_bwd_args &a, hipStream_t s) {
     const int nmb = (a.lse_seqlen + DqCfg<HD>::BM - 1) / DqCfg<HD>::BM;
     const int64_t grid = int64_t(nmb) * a.batch * a.nheads;
     if (grid == 0) return FA_OK;
+    if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
     hipLaunchKernelGGL((bwd_dq_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a, nmb);
     return int(hipGetLastError());
 }

@@ -73,51 +73,12 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
 
 // ---------------------------------------------------------------------------
-// LDS tiles.  All tiles are addressed in 16-byte chunks with an XOR swizzle on
-// the low 3 bits of the chunk index so that the MFMA operand reads (32 rows,
-// same logical chunk) and the staging writes are bank-conflict free.
-
-// Natural tile [rows][D] fp16: operand reads touch rows sigma(0..31).
-__device__ __forceinline__ int swz_nat(int row) {
-    const int r = row & 3;
-    return ((row >> 2) & 7) ^ ((r & 1) | ((r & 2) << 1));
-}
-template <int D>
-__device__ __forceinline__ int nat_off(int row, int chunk) {
-    return row * (D * 2) + ((chunk ^ swz_nat(row)) << 4);
-}
-// Transposed tile [X][R] fp16 (element (x, k) = source row k, column x):
-// operand reads touch x = 0..31 consecutive at one key chunk.
-template <int R>
-__device__ __forceinline__ int tr_off(int x, int kchunk) {
-    return x * (R * 2) + ((kchunk ^ (x & (R / 8 - 1) & 7)) << 4);
-}
+// LDS tiles are addressed in 16-byte chunks with an XOR swizzle of the chunk
+// index (swz below), so MFMA operand reads and transposed reads are
+// bank-conflict free.
 
 __device__ __forceinline__ f16x8 lds_ld16(const char *base, int off) {
     return *reinterpret_cast<const f16x8 *>(base + off);
-}
-__device__ __forceinline__ void lds_st16(char *base, int off, const u32x4 v) {
-    *reinterpret_cast<u32x4 *>(base + off) = v;
-}
-
-// Write 4 source rows (k0..k0+3, 8 columns x0..x0+7 each, one u32x4 per row)
-// into a transposed tile [X][R]: column x0+j receives the 4 halves of rows
-// k0..k0+3 as one 8-byte store.
-template <int R>
-__device__ __forceinline__ void tr_store4(char *base, int k0, int x0, const u32x4 r0, const u32x4 r1,
-                                          const u32x4 r2, const u32x4 r3) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const uint32_t a = r0[p], b = r1[p], c = r2[p], d = r3[p];
-        u32x2 lo, hi;
-        lo[0] = (a & 0xffffu) | (b << 16);
-        lo[1] = (c & 0xffffu) | (d << 16);
-        hi[0] = (a >> 16) | (b & 0xffff0000u);
-        hi[1] = (c >> 16) | (d & 0xffff0000u);
-        const int xa = x0 + 2 * p, xb = xa + 1;
-        *reinterpret_cast<u32x2 *>(base + tr_off<R>(xa, k0 >> 3) + ((k0 & 4) << 1)) = lo;
-        *reinterpret_cast<u32x2 *>(base + tr_off<R>(xb, k0 >> 3) + ((k0 & 4) << 1)) = hi;
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -209,21 +170,6 @@ __device__ __forceinline__ void g2l4_to(const void *g, uint32_t l) {
         : "v"(g), "s"(__builtin_amdgcn_readfirstlane(l))
         : "memory");
 }
-// global_load_lds_dword: lane l's 4 bytes at `g` land at lds_base + 4*l.
-__device__ __forceinline__ void g2l4(const void *g, char *lds_base) {
-    const uint32_t l =
-        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds_base);
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dword %1, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(g), "s"(l)
-        : "memory");
-}
-
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // s_waitcnt lgkmcnt(0): every LDS read issued so far has returned its data.
@@ -264,19 +210,6 @@ __device__ __forceinline__ int swz(int row) {
 template <int HD>
 __device__ __forceinline__ int tile_off(int row, int chunk) {
     return row * (HD * 2) + ((chunk ^ swz<HD / 8>(row)) << 4);
-}
-
-// MFMA A operand (32 x 16 fp16) of the transposed tile: lane (m, h) gets
-// column d0 + m of rows r0 + 8h + 0..7 (the key / query order a chained
-// accumulator supplies, see the header comment).
-template <int HD>
-__device__ __forceinline__ f16x8 lds_tr_operand(const char *tile, int r0, int d0, int lane) {
-    const int j = (lane & 15) >> 2, q = lane & 3, db = (lane >> 4) & 1, h = lane >> 5;
-    const int row = r0 + 8 * h + j, col = d0 + 16 * db + 4 * q;
-    const int byte = (col & 7) * 2;
-    const f16x4 lo = lds_tr4(tile, tile_off<HD>(row, col >> 3) + byte);
-    const f16x4 hi = lds_tr4(tile, tile_off<HD>(row + 4, col >> 3) + byte);
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // Copy rows [row0, row0 + ROWS) of a [rows][HD] fp16 source (row stride rs,

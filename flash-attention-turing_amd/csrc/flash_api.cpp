@@ -80,6 +80,12 @@ inline fa_tensor desc3(const at::Tensor &t) {  // packed [total][head][d]
     return fa_tensor{t.data_ptr(), 0, t.stride(0), t.stride(1)};
 }
 
+// Sizes go to the kernels as int32 (their index math is 64-bit where products can overflow).
+inline int32_t i32(int64_t v, const char *what) {
+    TORCH_CHECK(v >= 0 && v <= INT32_MAX, what, " must be below 2^31");
+    return int32_t(v);
+}
+
 inline hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); }
 
 inline void check_rc(int rc, const char *what) {
@@ -124,13 +130,13 @@ std::vector<at::Tensor> mha_fwd(at::Tensor q, at::Tensor k, at::Tensor v, const 
     a.v = desc4(v);
     a.o = desc4(o);
     a.lse = l.data_ptr<float>();
-    a.batch = int32_t(batch_size);
-    a.seqlen_q = int32_t(seqlen_q);
-    a.seqlen_k = int32_t(seqlen_k);
-    a.nheads = int32_t(num_heads);
-    a.nheads_k = int32_t(num_heads_k);
+    a.batch = i32(batch_size, "batch_size");
+    a.seqlen_q = i32(seqlen_q, "seqlen_q");
+    a.seqlen_k = i32(seqlen_k, "seqlen_k");
+    a.nheads = i32(num_heads, "num_heads");
+    a.nheads_k = i32(num_heads_k, "num_heads_k");
     a.head_dim = int32_t(head_size);
-    a.lse_seqlen = int32_t(seqlen_q);
+    a.lse_seqlen = i32(seqlen_q, "seqlen_q");
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
     check_rc(fa_fwd(&a, current_stream()), "fa_fwd");
@@ -177,13 +183,13 @@ std::vector<at::Tensor> mha_bwd(at::Tensor q, at::Tensor k, at::Tensor v, at::Te
     a.dv = desc4(dv.buf);
     a.lse = l.data_ptr<float>();
     a.dsum = dsum.data_ptr<float>();
-    a.batch = int32_t(batch_size);
-    a.seqlen_q = int32_t(seqlen_q);
-    a.seqlen_k = int32_t(seqlen_k);
-    a.nheads = int32_t(num_heads);
-    a.nheads_k = int32_t(num_heads_k);
+    a.batch = i32(batch_size, "batch_size");
+    a.seqlen_q = i32(seqlen_q, "seqlen_q");
+    a.seqlen_k = i32(seqlen_k, "seqlen_k");
+    a.nheads = i32(num_heads, "num_heads");
+    a.nheads_k = i32(num_heads_k, "num_heads_k");
     a.head_dim = int32_t(head_size);
-    a.lse_seqlen = int32_t(seqlen_q);
+    a.lse_seqlen = i32(seqlen_q, "seqlen_q");
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
     check_rc(fa_bwd(&a, current_stream()), "fa_bwd");
@@ -242,11 +248,11 @@ std::vector<at::Tensor> mha_varlen_fwd(at::Tensor q, at::Tensor k, at::Tensor v,
     a.lse = l.data_ptr<float>();
     a.cu_seqlens_q = cu_seqlens_q.data_ptr<int32_t>();
     a.cu_seqlens_k = cu_seqlens_k.data_ptr<int32_t>();
-    a.batch = int32_t(batch_size);
+    a.batch = i32(batch_size, "batch_size");
     a.seqlen_q = max_seqlen_q;
     a.seqlen_k = max_seqlen_k;
-    a.nheads = int32_t(num_heads);
-    a.nheads_k = int32_t(num_heads_k);
+    a.nheads = i32(num_heads, "num_heads");
+    a.nheads_k = i32(num_heads_k, "num_heads_k");
     a.head_dim = int32_t(head_size);
     a.lse_seqlen = max_seqlen_q;
     a.softmax_scale = softmax_scale;
@@ -299,11 +305,11 @@ std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v,
     a.dsum = dsum.data_ptr<float>();
     a.cu_seqlens_q = cu_seqlens_q.data_ptr<int32_t>();
     a.cu_seqlens_k = cu_seqlens_k.data_ptr<int32_t>();
-    a.batch = int32_t(batch_size);
+    a.batch = i32(batch_size, "batch_size");
     a.seqlen_q = max_seqlen_q;
     a.seqlen_k = max_seqlen_k;
-    a.nheads = int32_t(num_heads);
-    a.nheads_k = int32_t(num_heads_k);
+    a.nheads = i32(num_heads, "num_heads");
+    a.nheads_k = i32(num_heads_k, "num_heads_k");
     a.head_dim = int32_t(head_size);
     a.lse_seqlen = max_seqlen_q;
     a.softmax_scale = softmax_scale;
@@ -462,18 +468,18 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     a.cache_batch_idx = has_cache_batch_idx ? cache_batch_idx.data_ptr<int32_t>() : nullptr;
     a.block_table = has_block_table ? block_table.data_ptr<int32_t>() : nullptr;
     a.block_table_stride = has_block_table ? block_table.stride(0) : 0;
-    a.batch = int32_t(batch_size);
-    a.seqlen_q = int32_t(seqlen_q);
-    a.nheads = int32_t(num_heads);
-    a.nheads_k = int32_t(num_heads_k);
+    a.batch = i32(batch_size, "batch_size");
+    a.seqlen_q = i32(seqlen_q, "seqlen_q");
+    a.nheads = i32(num_heads, "num_heads");
+    a.nheads_k = i32(num_heads_k, "num_heads_k");
     a.head_dim = int32_t(head_size);
-    a.seqlen_new = int32_t(seqlen_new);
+    a.seqlen_new = i32(seqlen_new, "seqlen_new");
     a.page_block_size = int32_t(page_block_size);
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
     a.num_splits = 1;
     a.cache_capacity = int32_t(seqlen_cache);
-    a.cache_batch = has_block_table ? 0 : int32_t(batch_size_cache);
+    a.cache_batch = has_block_table ? 0 : i32(batch_size_cache, "cache batch size");
     a.status = status;
     // Upstream's normalisation: a bound at least the cache capacity is no bound.
     if (window_size_left >= seqlen_cache) window_size_left = -1;
@@ -522,8 +528,11 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
         TORCH_CHECK(seqlen_ro >= 1 && seqlen_ro <= INT32_MAX, "rotary_cos must have at least one row");
         if (has_block_table)
             TORCH_CHECK(seqlen_ro >= seqlen_cache, "cos/sin seqlen must be at least the seqlen of KV cache");
-        cos_t = aligned(cos_t);
-        sin_t = aligned(sin_t);
+        // The kernels read angle row p at p * rotary_dim / 2 (packed rows): a
+        // view with any other row stride (a column slice of a wider table) is
+        // copied first.
+        cos_t = aligned(cos_t.contiguous());
+        sin_t = aligned(sin_t.contiguous());
         a.rotary_cos = cos_t.data_ptr();
         a.rotary_sin = sin_t.data_ptr();
         a.rotary_dim = int32_t(rotary_dim);
@@ -567,16 +576,16 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     f.seqused_k = cache_seqlens.data_ptr<int32_t>();
     f.seqused_k_add = int32_t(seqlen_new);
     f.k_batch_idx = a.cache_batch_idx;
-    f.batch = int32_t(batch_size);
-    f.seqlen_q = int32_t(seqlen_q);
+    f.batch = i32(batch_size, "batch_size");
+    f.seqlen_q = i32(seqlen_q, "seqlen_q");
     f.seqlen_k = int32_t(seqlen_cache);
-    f.nheads = int32_t(num_heads);
-    f.nheads_k = int32_t(num_heads_k);
+    f.nheads = i32(num_heads, "num_heads");
+    f.nheads_k = i32(num_heads_k, "num_heads_k");
     f.head_dim = int32_t(head_size);
-    f.lse_seqlen = int32_t(seqlen_q);
+    f.lse_seqlen = i32(seqlen_q, "seqlen_q");
     f.softmax_scale = softmax_scale;
     f.causal = is_causal ? 1 : 0;
-    f.k_batch = int32_t(batch_size_cache);
+    f.k_batch = i32(batch_size_cache, "cache batch size");
     f.status = status;
     check_rc(fa_fwd(&f, stream), "fa_fwd (kv-cache chunk)");
     return {out, lse};

@@ -72,3 +72,169 @@ def cu_from_lengths(lengths: Sequence[int]) -> torch.Tensor:
     for n in lengths:
         cu.append(cu[-1] + int(n))
     return torch.tensor(cu, dtype=torch.int32)
+
+
+def check_fwd_bwd(tag, q, k, v, do, out, lse, grads, scale, causal, kv_chunk=None, log=None):
+    """Check one independent slice (whole batch rows) of a dense forward (and
+    backward when ``grads`` = (dq, dk, dv) is given) against the fp32 oracle,
+    bounded by 2x the rounding-point twin's error, KV head group by KV head
+    group (``kv_chunk`` KV heads at a time) so the oracle's [h, sq, sk]
+    intermediates stay small at long sequences.
+
+    The bound uses the twin's error over the whole slice, as an unchunked
+    check would: per chunk the largest error, the twin's largest error and
+    the largest (error - fp32 noise) are kept, and the bounds are applied
+    once every chunk is done.  Returns {tensor: {"err", "err_ref", "bound",
+    "noise_max"}} for margin reports."""
+    from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise
+    from oracle.twin import bwd_twin, fwd_twin
+
+    hk = k.shape[2]
+    groups = q.shape[2] // hk
+    kv_chunk = kv_chunk or hk
+    names = ["out"] + (["dq", "dk", "dv"] if grads is not None else [])
+    acc = {n: {"err": 0.0, "err_ref": 0.0, "dmn": -math.inf, "noise_max": 0.0} for n in names}
+    lse_err = 0.0
+    for c0 in range(0, hk, kv_chunk):
+        c1 = min(hk, c0 + kv_chunk)
+        hq = slice(c0 * groups, c1 * groups)
+        hkv = slice(c0, c1)
+        qc, kc, vc = q[:, :, hq], k[:, :, hkv], v[:, :, hkv]
+        o_ref, l_ref = attention_fwd(qc, kc, vc, scale, causal)
+        o_tw, l_tw = fwd_twin(qc, kc, vc, scale, causal)
+        parts = {"out": (out[:, :, hq], o_ref, o_tw, None)}
+        if lse is not None:
+            lse_err = max(lse_err, assert_lse(lse[:, hq], l_ref))
+        if grads is not None:
+            doc = do[:, :, hq]
+            g_ref = attention_bwd(qc, kc, vc, o_ref, l_ref, doc, scale, causal)
+            g_tw = bwd_twin(qc, kc, vc, o_tw, l_tw, doc, scale, causal)
+            noise = bwd_fp32_noise(qc, kc, vc, o_ref, l_ref, doc, scale, causal, dt=torch.float32)
+            for i, (n, sl) in enumerate((("dq", hq), ("dk", hkv), ("dv", hkv))):
+                parts[n] = (grads[i][:, :, sl], g_ref[i], g_tw[i], noise[i])
+        for n, (got, ref, tw, nz) in parts.items():
+            diff = (got.float().cpu() - ref.float().cpu()).abs()
+            a = acc[n]
+            assert math.isfinite(diff.max().item()), f"{tag} {n}: non-finite output"
+            a["err"] = max(a["err"], diff.max().item())
+            a["err_ref"] = max(a["err_ref"], max_abs(tw, ref))
+            if nz is not None:
+                a["dmn"] = max(a["dmn"], (diff - nz.float().cpu()).max().item())
+                a["noise_max"] = max(a["noise_max"], nz.max().item())
+        if log:
+            log(f"{tag}: KV heads {c0}-{c1 - 1} checked")
+    out_stats = {}
+    for n, a in acc.items():
+        bound = bound_2x(a["err_ref"])
+        if n == "out":
+            assert a["err"] <= bound, f"{tag} {n}: max-abs {a['err']:.3e} > 2 x reference-twin error {a['err_ref']:.3e}"
+        else:
+            assert a["dmn"] <= bound, (
+                f"{tag} {n}: max-abs {a['err']:.3e} exceeds 2 x reference-twin error {a['err_ref']:.3e} + fp32 noise "
+                f"by {a['dmn'] - bound:.3e}"
+            )
+        out_stats[n] = {"err": a["err"], "err_ref": a["err_ref"], "bound": bound, "noise_max": a["noise_max"]}
+    if lse is not None:
+        out_stats["lse"] = {"err": lse_err}
+    return out_stats
+
+
+# Seeded inputs of the full-size parity tests (shared with tests/golden/make_ref_error.py,
+# which records the twin's error on exactly these tensors).
+def dense_inputs(b, s, h, d, seed, hk=None, n=4):
+    """q, k, v, dO drawn in that order from one CPU generator (k, v with hk heads)."""
+    g = torch.Generator().manual_seed(seed)
+    hk = hk or h
+    shapes = [(b, s, h, d), (b, s, hk, d), (b, s, hk, d), (b, s, h, d)][:n]
+    return [randn16(sh, g) for sh in shapes]
+
+
+def c3_inputs():
+    """Config c3's shape: 16 packed causal sequences, lengths uniform in [128, 4096], 32 / 8 heads, d 128."""
+    h, hk, d = 32, 8, 128
+    lens = varlen_lengths(16, 128, 4096, seed=13)
+    cu = cu_from_lengths(lens)
+    total = int(cu[-1])
+    g = torch.Generator().manual_seed(14)
+    q = randn16((total, h, d), g)
+    k = randn16((total, hk, d), g)
+    v = randn16((total, hk, d), g)
+    do = randn16((total, h, d), g)
+    return lens, cu, q, k, v, do
+
+
+def c3_checked_sequences(lens):
+    """The shortest, the median-length and the longest sequence."""
+    order = sorted(range(len(lens)), key=lambda i: lens[i])
+    return [order[0], order[len(order) // 2], order[-1]]
+
+
+# Full-size configurations: (b, s, h, d, seed, causal, checked units).  A unit is
+# (batch row, first head, end head): every element of those heads of that row.
+FULLSIZE = {
+    "c2": (4, 4096, 16, 128, 12, True, ((0, 0, 16), (3, 0, 16))),
+    "s8192": (4, 8192, 16, 128, 17, True, ((0, 0, 8), (0, 8, 16), (3, 0, 8), (3, 8, 16))),
+}
+
+
+def unit_key(name, unit):
+    row, h0, h1 = unit
+    h = FULLSIZE[name][2]
+    return f"{name}_row{row}" if (h0, h1) == (0, h) else f"{name}_row{row}_h{h0}-{h1 - 1}"
+
+
+def check_varlen(tag, cu_q, cu_k, q, k, v, do, out, lse, grads, scale, causal):
+    """Packed varlen forward (and backward when ``grads`` is given) against the
+    per-sequence oracle, 2x the twin's error over the whole batch (the fp32
+    noise widening for the gradients), LSE [b, h, max_seqlen_q] including its
+    zero padding.  Rows of out / grads outside every sequence are not checked."""
+    from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise
+    from oracle.twin import bwd_twin, fwd_twin
+
+    nb = cu_q.numel() - 1
+    h = q.shape[1]
+    o_ref, o_tw = torch.zeros(q.shape), torch.zeros(q.shape, dtype=torch.float16)
+    mq = max(int(cu_q[i + 1] - cu_q[i]) for i in range(nb))
+    lse_ref = torch.zeros((nb, h, mq))
+    g_ref = [torch.zeros(t.shape) for t in (q, k, v)]
+    g_tw = [torch.zeros(t.shape) for t in (q, k, v)]
+    g_nz = [torch.zeros(t.shape) for t in (q, k, v)]
+    for b in range(nb):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        qb, kb, vb = q[q0:q1][None], k[k0:k1][None], v[k0:k1][None]
+        ob, lb = attention_fwd(qb, kb, vb, scale, causal)
+        otb, ltb = fwd_twin(qb, kb, vb, scale, causal)
+        o_ref[q0:q1], o_tw[q0:q1], lse_ref[b, :, : q1 - q0] = ob[0], otb[0], lb[0]
+        if grads is not None:
+            dob = do[q0:q1][None]
+            gr = attention_bwd(qb, kb, vb, ob, lb, dob, scale, causal)
+            gt = bwd_twin(qb, kb, vb, otb, ltb, dob, scale, causal)
+            gn = bwd_fp32_noise(qb, kb, vb, ob, lb, dob, scale, causal)
+            for i, (lo, hi) in enumerate([(q0, q1), (k0, k1), (k0, k1)]):
+                g_ref[i][lo:hi], g_tw[i][lo:hi], g_nz[i][lo:hi] = gr[i][0], gt[i][0].float(), gn[i][0]
+    tq, tk = int(cu_q[-1]), int(cu_k[-1])
+    res = {"out": assert_2x(f"{tag} out", out[:tq], o_ref[:tq], o_tw[:tq])}
+    if lse is not None:
+        res["lse"] = assert_lse(lse, lse_ref)
+    if grads is not None:
+        for i, (n, t) in enumerate((("dq", tq), ("dk", tk), ("dv", tk))):
+            res[n] = assert_2x(f"{tag} {n}", grads[i][:t], g_ref[i][:t], g_tw[i][:t], g_nz[i][:t])
+    return res
+
+
+def kv_oracle(q, kc, vc, k, v, seqlens, batch_idx, table, causal, splits, scale):
+    """Append k / v as the reference does (contiguous, remapped or paged), then
+    split-KV attention over the logical caches.  Returns (out, lse, k_cache, v_cache)."""
+    from oracle import kvcache as okv
+
+    kc, vc = kc.clone(), vc.clone()
+    if k is not None:
+        if table is None:
+            okv.append_contiguous(kc, vc, k, v, seqlens, batch_idx)
+        else:
+            okv.append_paged(kc, vc, k, v, seqlens, table)
+    ends = seqlens + (0 if k is None else k.shape[1])
+    ku, vu = okv.materialize(kc, vc, ends, batch_idx, table)
+    s = q.shape[-1] ** -0.5 if scale is None else scale
+    out, lse = okv.splitkv_attention(q, ku, vu, ends, s, causal, max(splits, 1))
+    return out, lse, kc, vc

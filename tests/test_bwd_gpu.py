@@ -38,6 +38,14 @@ def _oracles(q, k, v, do, s, causal):
     return grads_ref, grads_tw, noise
 
 
+def _check_grads(tag, q, k, v, do, grads, s, causal):
+    """Gradients (any layout: packed slices, caller tensors) against the oracle."""
+    qc, kc, vc, doc = (t.detach().cpu() for t in (q, k, v, do))
+    g_ref, g_tw, noise = _oracles(qc, kc, vc, doc, s, causal)
+    for name, got, r, t, n in zip(("dq", "dk", "dv"), grads, g_ref, g_tw, noise):
+        assert_2x(f"{tag} {name}", got, r, t, n)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("hd,causal,sq,sk,heads,batch,scale", CASES)
 def test_bwd_parity(device, hd, causal, sq, sk, heads, batch, scale):
@@ -70,6 +78,7 @@ def test_bwd_packed_matches_unpacked(device):
     assert torch.equal(qkv.grad[:, :, 0], q.grad)
     assert torch.equal(qkv.grad[:, :, 1], k.grad)
     assert torch.equal(qkv.grad[:, :, 2], v.grad)
+    _check_grads("qkvpacked", q, k, v, do, [qkv.grad[:, :, i] for i in range(3)], 64 ** -0.5, True)
 
 
 @pytest.mark.gpu
@@ -101,6 +110,7 @@ def test_kvpacked_bwd_matches_unpacked(device):
     assert torch.equal(q.grad, qr.grad)
     assert torch.equal(kv.grad[:, :, 0], k.grad)
     assert torch.equal(kv.grad[:, :, 1], v.grad)
+    _check_grads("kvpacked", q, k, v, do, [q.grad, kv.grad[:, :, 0], kv.grad[:, :, 1]], 128 ** -0.5, True)
 
 
 @pytest.mark.gpu
@@ -120,6 +130,7 @@ def test_bwd_into_given_tensors(device):
     for r, x, w in zip(ref, got, views):
         assert x.data_ptr() == w.data_ptr()
         assert torch.equal(x, r)
+    _check_grads("into packed slices", q, k, v, do, got, s, True)
     buf = torch.zeros(1 * 96 * 2 * 64 + 4, dtype=torch.float16, device=device)
     odd = buf[4:].view(1, 96, 2, 64)  # base 8 bytes past a 16-byte boundary
     dq, _, _ = fai._flash_attn_backward(do, q, k, v, out, lse, s, True, odd, None, None)

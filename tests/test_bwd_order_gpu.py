@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import fa_capi
-from helpers import cu_from_lengths, randn16
+from helpers import check_varlen, cu_from_lengths, randn16
 
 CASES = [
     # lengths_q, lengths_k, h, hk, hd, causal
@@ -80,3 +80,6 @@ def test_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, hd, c
             assert all(x >= y for x, y in zip(buckets, buckets[1:])), "items must come most rows first"
     for a, b, name in zip(grads[False], grads[True], ("dq", "dk", "dv")):
         assert torch.equal(a, b), f"{name} differs between the natural and the device-built order"
+    # Both orders' results (bit-identical) against the per-sequence oracle.
+    check_varlen("work order", cu_q, cu_k, q.cpu(), k.cpu(), v.cpu(), do.cpu(), o.cpu(), lse.cpu(), grads[True], s,
+                 causal)

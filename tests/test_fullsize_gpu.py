@@ -1,13 +1,16 @@
-"""Parity at the BASELINE configurations' full sizes (c1-c5), on the GPU.
+"""Parity at the BASELINE configurations' full sizes (c1-c5) and at the
+north-star point (causal b4 s8192 h16 d128), on the GPU.
 
 The kernels run on the whole workload; the fp32 oracle and the
 rounding-point twin are evaluated on the CPU for the parts that finish in
 seconds there:
 
 * c1 (b2 s512 h8 d64, non-causal forward): every element;
-* c2 (b4 s4096 h16 d128 causal, forward + backward): every element of batch
-  rows 0 and 3 (rows of a batch are independent, so each is the full
-  computation of that row at the full sequence length and head count);
+* c2 (b4 s4096 h16 d128 causal, forward + backward) and the s8192 point:
+  every element of batch rows 0 and 3 (rows of a batch are independent, so
+  each is the full computation of that row at the full sequence length and
+  head count), checked four KV heads at a time (the s8192 rows as two tests
+  of eight heads each);
 * c3 (16 packed causal sequences, 32/8 heads): every element of the shortest,
   the median-length and the longest sequence;
 * c4 (paged decode with append, 64 sequences up to 32k keys, 8 splits) and c5
@@ -16,87 +19,114 @@ seconds there:
   position unchanged.
 
 Bounds as in the small-size tests: 2x the twin's error (+ the fp32 noise
-floor for the backward), LSE to 2e-5 relative, bit-exact cache writes.
+floor for the backward), LSE to 2e-5 relative, bit-exact cache writes.  The
+twin's error on these exact inputs is committed in tests/golden/ref_error.json
+(tests/golden/make_ref_error.py); each test checks that the twin still
+reproduces it (within 5 %), so a change to the twin's rounding points cannot
+silently move the bound, and that the fp32-noise widening of the backward
+bound stays below a tenth of the 2x bound.
 """
 
+import json
+import os
 import time
 
 import pytest
 import torch
 
 import flash_attention_interface as fai
-from helpers import assert_2x, assert_lse, cu_from_lengths, randn16, varlen_lengths
+from helpers import (FULLSIZE, assert_2x, assert_lse, c3_checked_sequences, c3_inputs, check_fwd_bwd, dense_inputs, randn16,
+                     unit_key)
 from oracle import kvcache as okv
-from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise
-from oracle.twin import bwd_twin, fwd_twin
+
+REF_ERROR = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_error.json")))
+TWIN_REL_TOL = 0.05  # the twin's error on the committed inputs, recomputed on another host's BLAS
+NOISE_FRAC = 0.1  # largest fp32-noise widening allowed, as a fraction of the 2x bound
 
 
 def _log(msg):
     print(f"[fullsize] {msg}", flush=True)
 
 
-def _check_fwd_bwd(tag, q, k, v, do, out, dq, dk, dv, scale, causal):
-    t = time.time()
-    o_ref, l_ref = attention_fwd(q, k, v, scale, causal)
-    o_tw, l_tw = fwd_twin(q, k, v, scale, causal)
-    assert_2x(f"{tag} out", out, o_ref, o_tw)
-    if dq is None:
-        _log(f"{tag}: forward checked in {time.time() - t:.1f} s")
-        return o_ref, l_ref
-    g_ref = attention_bwd(q, k, v, o_ref, l_ref, do, scale, causal)
-    g_tw = bwd_twin(q, k, v, o_tw, l_tw, do, scale, causal)
-    noise = bwd_fp32_noise(q, k, v, o_ref, l_ref, do, scale, causal, dt=torch.float32)
-    for name, got, r, tw, nz in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref, g_tw, noise):
-        assert_2x(f"{tag} {name}", got, r, tw, nz)
-    _log(f"{tag}: forward and backward checked in {time.time() - t:.1f} s")
-    return o_ref, l_ref
+def _check_against_fixture(key, stats):
+    """The twin's error equals the committed one; the noise widening is small; log the margins."""
+    fx = REF_ERROR[key]
+    for n, s in stats.items():
+        if n == "lse":
+            continue
+        want = fx["err_ref"][n]
+        assert abs(s["err_ref"] - want) <= TWIN_REL_TOL * want, (
+            f"{key} {n}: twin error {s['err_ref']:.4e} differs from the committed {want:.4e}"
+        )
+        if s["noise_max"]:
+            assert s["noise_max"] <= NOISE_FRAC * s["bound"], (
+                f"{key} {n}: fp32-noise widening {s['noise_max']:.3e} above {NOISE_FRAC} of the bound {s['bound']:.3e}"
+            )
+    _log(f"{key} margins (err / 2x bound): " + ", ".join(
+        f"{n} {s['err'] / s['bound']:.2f}" for n, s in stats.items() if n != "lse"))
 
 
 @pytest.mark.gpu
 def test_c1_full_forward(device):
-    g = torch.Generator().manual_seed(11)
-    q, k, v = (randn16((2, 512, 8, 64), g) for _ in range(3))
+    q, k, v = dense_inputs(2, 512, 8, 64, 11, n=3)
     _log("c1: b2 s512 h8 d64 non-causal")
     out, lse = fai._flash_attn_forward(q.to(device), k.to(device), v.to(device), 64 ** -0.5, False)
     torch.cuda.synchronize()
-    _, l_ref = _check_fwd_bwd("c1", q, k, v, None, out.cpu(), None, None, None, 64 ** -0.5, False)
-    assert_lse(lse.cpu(), l_ref)
+    stats = check_fwd_bwd("c1", q, k, v, None, out.cpu(), lse.cpu(), None, 64 ** -0.5, False)
+    _check_against_fixture("c1", stats)
+
+
+_DENSE = {}
+
+
+def _dense_run(device, name):
+    """Forward (autograd) + backward of a full-size dense configuration on the GPU, once per module."""
+    if name not in _DENSE:
+        b, s, h, d, seed, causal, _ = FULLSIZE[name]
+        q, k, v, do = dense_inputs(b, s, h, d, seed)
+        _log(f"{name}: b{b} s{s} h{h} d{d} causal={causal} fwd + bwd on the GPU")
+        qd, kd, vd = (t.to(device).requires_grad_() for t in (q, k, v))
+        out = fai.flash_attn_func(qd, kd, vd, causal=causal)
+        out.backward(do.to(device))
+        # The same forward again for its LSE (the kernels are deterministic).
+        out2, lse = fai._flash_attn_forward(qd.detach(), kd.detach(), vd.detach(), d ** -0.5, causal)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out.detach())
+        assert all(torch.isfinite(t).all() for t in (out, qd.grad, kd.grad, vd.grad))
+        _DENSE.clear()  # one configuration's tensors at a time
+        _DENSE[name] = (q, k, v, do, out.detach().cpu(), lse.cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu())
+    return _DENSE[name]
+
+
+def _check_dense_unit(device, name, unit):
+    b, s, h, d, seed, causal, _ = FULLSIZE[name]
+    q, k, v, do, out, lse, dq, dk, dv = _dense_run(device, name)
+    r, hs = slice(unit[0], unit[0] + 1), slice(unit[1], unit[2])
+    key = unit_key(name, unit)
+    t = time.time()
+    stats = check_fwd_bwd(key, q[r, :, hs], k[r, :, hs], v[r, :, hs], do[r, :, hs], out[r, :, hs], lse[r, hs],
+                          (dq[r, :, hs], dk[r, :, hs], dv[r, :, hs]), d ** -0.5, causal, kv_chunk=4, log=_log)
+    _log(f"{key}: forward and backward checked in {time.time() - t:.1f} s")
+    _check_against_fixture(key, stats)
 
 
 @pytest.mark.gpu
-def test_c2_full_forward_backward(device):
-    b, s, h, d = 4, 4096, 16, 128
-    g = torch.Generator().manual_seed(12)
-    q, k, v, do = (randn16((b, s, h, d), g) for _ in range(4))
-    _log("c2: b4 s4096 h16 d128 causal fwd + bwd on the GPU")
-    qd, kd, vd = (t.to(device).requires_grad_() for t in (q, k, v))
-    out = fai.flash_attn_func(qd, kd, vd, causal=True)
-    out.backward(do.to(device))
-    # The same forward again for its LSE (the kernels are deterministic).
-    out2, lse = fai._flash_attn_forward(qd.detach(), kd.detach(), vd.detach(), d ** -0.5, True)
-    torch.cuda.synchronize()
-    assert torch.equal(out2, out.detach())
-    assert all(torch.isfinite(t).all() for t in (out, qd.grad, kd.grad, vd.grad))
-    for r in (0, 3):  # checked batch rows
-        sl = slice(r, r + 1)
-        _, l_ref = _check_fwd_bwd(
-            f"c2 row {r}", q[sl], k[sl], v[sl], do[sl], out.detach()[sl].cpu(), qd.grad[sl].cpu(),
-            kd.grad[sl].cpu(), vd.grad[sl].cpu(), d ** -0.5, True,
-        )
-        assert_lse(lse[sl].cpu(), l_ref)
+@pytest.mark.parametrize("unit", FULLSIZE["c2"][6])
+def test_c2_full_forward_backward(device, unit):
+    _check_dense_unit(device, "c2", unit)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("unit", FULLSIZE["s8192"][6])
+def test_s8192_north_star_forward_backward(device, unit):
+    """The shape the north star's MFMA targets are quoted on (benchmark.sh:17-21)."""
+    _check_dense_unit(device, "s8192", unit)
 
 
 @pytest.mark.gpu
 def test_c3_full_varlen_gqa(device):
-    h, hk, d = 32, 8, 128
-    lens = varlen_lengths(16, 128, 4096, seed=13)
-    cu = cu_from_lengths(lens)
-    total, mx = int(cu[-1]), max(lens)
-    g = torch.Generator().manual_seed(14)
-    q = randn16((total, h, d), g)
-    k = randn16((total, hk, d), g)
-    v = randn16((total, hk, d), g)
-    do = randn16((total, h, d), g)
+    lens, cu, q, k, v, do = c3_inputs()
+    total, mx, d = int(cu[-1]), max(lens), q.shape[-1]
     _log(f"c3: 16 packed causal sequences ({total} tokens, max {mx}), 32/8 heads, fwd + bwd on the GPU")
     qd, kd, vd = (t.to(device).requires_grad_() for t in (q, k, v))
     cud = cu.to(device)
@@ -105,15 +135,15 @@ def test_c3_full_varlen_gqa(device):
     out2, lse = fai._flash_attn_varlen_forward(qd.detach(), kd.detach(), vd.detach(), cud, cud, mx, mx, d ** -0.5, True)
     torch.cuda.synchronize()
     assert torch.equal(out2, out.detach())
-    order = sorted(range(16), key=lambda i: lens[i])
-    for i in (order[0], order[8], order[-1]):
+    out, lse = out.detach().cpu(), lse.cpu()
+    dq, dk, dv = qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu()
+    for i in c3_checked_sequences(lens):
         a, e = int(cu[i]), int(cu[i + 1])
-        _, l_ref = _check_fwd_bwd(
-            f"c3 seq {i} (n={e - a})", q[a:e][None], k[a:e][None], v[a:e][None], do[a:e][None],
-            out.detach()[a:e][None].cpu(), qd.grad[a:e][None].cpu(), kd.grad[a:e][None].cpu(), vd.grad[a:e][None].cpu(),
-            d ** -0.5, True,
+        stats = check_fwd_bwd(
+            f"c3 seq {i} (n={e - a})", q[a:e][None], k[a:e][None], v[a:e][None], do[a:e][None], out[a:e][None],
+            lse[i : i + 1, :, : e - a], (dq[a:e][None], dk[a:e][None], dv[a:e][None]), d ** -0.5, True, kv_chunk=4,
         )
-        assert_lse(lse[i : i + 1, :, : e - a].cpu(), l_ref)
+        _check_against_fixture(f"c3_seq{i}", stats)
 
 
 def _check_kvcache(tag, device, q, k_cache, v_cache, k_new, v_new, seqlens, batch_idx, table, splits):

@@ -81,6 +81,11 @@ def test_fwd_public_api_and_packed(device):
     kv = qkv[:, :, 1:]
     out_kv = fai.flash_attn_kvpacked_func(q, kv, causal=True)
     assert torch.equal(out_kv, out)
+    qc, kc, vc = (t.cpu() for t in (q, k, v))
+    o_ref, _ = attention_fwd(qc, kc, vc, 128 ** -0.5, True)
+    o_tw, _ = fwd_twin(qc, kc, vc, 128 ** -0.5, True)
+    assert_2x("qkvpacked out", out_packed, o_ref, o_tw)
+    assert_2x("kvpacked out", out_kv, o_ref, o_tw)
 
 
 @pytest.mark.gpu
@@ -92,6 +97,9 @@ def test_fwd_strided_views(device):
     out = fai.flash_attn_func(q, k, v)
     out_c = fai.flash_attn_func(q.contiguous(), k.contiguous(), v.contiguous())
     assert torch.equal(out, out_c)
+    qc, kc, vc = (t.cpu() for t in (q, k, v))
+    o_ref, _ = attention_fwd(qc, kc, vc, 64 ** -0.5, False)
+    assert_2x("strided out", out, o_ref, fwd_twin(qc, kc, vc, 64 ** -0.5, False)[0])
 
 
 @pytest.mark.gpu

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import flash_attention_interface as fai
-from helpers import assert_2x, assert_lse, randn16
+from helpers import assert_2x, assert_lse, kv_oracle, randn16
 from oracle import kvcache as okv
 
 
@@ -55,18 +55,7 @@ def _run(device, q, kc, vc, k, v, seqlens, batch_idx, table, causal, splits, sca
     return out.cpu(), lse.cpu(), kcd.cpu(), vcd.cpu()
 
 
-def _oracle(q, kc, vc, k, v, seqlens, batch_idx, table, causal, splits, scale):
-    kc, vc = kc.clone(), vc.clone()
-    if k is not None:
-        if table is None:
-            okv.append_contiguous(kc, vc, k, v, seqlens, batch_idx)
-        else:
-            okv.append_paged(kc, vc, k, v, seqlens, table)
-    ends = seqlens + (0 if k is None else k.shape[1])
-    ku, vu = okv.materialize(kc, vc, ends, batch_idx, table)
-    s = q.shape[-1] ** -0.5 if scale is None else scale
-    out, lse = okv.splitkv_attention(q, ku, vu, ends, s, causal, max(splits, 1))
-    return out, lse, kc, vc
+_oracle = kv_oracle
 
 
 CASES = [

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import flash_attention_interface as fai
-from helpers import randn16
+from helpers import assert_2x, assert_lse, kv_oracle, randn16
 
 
 def _inputs(b, sq, h, hk, hd, cap, new, gen, paged=False, page=256):
@@ -73,6 +73,11 @@ def test_nosync_matches_default(device, b, sq, h, hk, hd, cap, new, paged, remap
     for name, r, x in zip(("out", "lse", "k_cache", "v_cache"), ref, got):
         assert torch.equal(r, x), name
     fai.flash_attn_kvcache_check(device)  # nothing recorded
+    # The sync-free results against the oracle directly.
+    o_ref, l_ref, kc_ref, vc_ref = kv_oracle(q, kc, vc, k, v, seqlens, batch_idx, table, True, splits, None)
+    assert torch.equal(got[2], kc_ref) and torch.equal(got[3], vc_ref), "append differs from the oracle"
+    assert_2x("out", got[0], o_ref, o_ref.to(torch.float16))
+    assert_lse(got[1], l_ref)
 
 
 @pytest.mark.gpu
@@ -85,6 +90,8 @@ def test_nosync_out_of_range_caught_on_device(device, route):
     q, kc, vc, k, v, table = _inputs(b, sq, h, hk, hd, cap, new, gen, paged)
     good = torch.tensor([100, 200, 50], dtype=torch.int32)
     ref = _call(device, q, kc, vc, k, v, good, table, None, splits, validate=True)
+    # Oracle rows for the sequences kept valid (0 and 2); the invalid one must read as no keys.
+    o_ref, l_ref, _, _ = kv_oracle(q, kc, vc, k, v, good, None, table, True, splits, None)
     fai.flash_attn_kvcache_check(device)
     for bad_len in (cap - new + 1, -1):
         seqlens = good.clone()
@@ -94,6 +101,9 @@ def test_nosync_out_of_range_caught_on_device(device, route):
                 _call(device, q, kc, vc, k, v, seqlens, table, None, splits, validate=True)
         out, lse, kcd, vcd = _call(device, q, kc, vc, k, v, seqlens, table, None, splits, validate=False)
         assert not out[1].any() and not lse[1].any()
+        for bi in (0, 2):
+            assert_2x(f"out[{bi}]", out[bi], o_ref[bi], o_ref[bi].to(torch.float16))
+            assert_lse(lse[bi], l_ref[bi])
         assert torch.equal(out[0], ref[0][0]) and torch.equal(out[2], ref[0][2])
         assert torch.equal(lse[0], ref[1][0]) and torch.equal(lse[2], ref[1][2])
         if paged:
@@ -125,6 +135,13 @@ def test_nosync_cache_row_out_of_range(device, splits, sq):
             _call(device, q, kc, vc, k, v, seqlens, None, idx, splits, validate=True)
         out, lse, kcd, vcd = _call(device, q, kc, vc, k, v, seqlens, None, idx, splits, validate=False)
         assert not out[1].any() and not lse[1].any()
+        # Sequences 0 and 2 (cache rows 2 and 0) against the oracle.
+        keep = torch.tensor([0, 2])
+        o_ref, l_ref, _, _ = kv_oracle(q[keep], kc, vc, k[keep], v[keep], seqlens[keep], idx[keep], None, True,
+                                       splits, None)
+        for j, bi in enumerate((0, 2)):
+            assert_2x(f"out[{bi}]", out[bi], o_ref[j], o_ref[j].to(torch.float16))
+            assert_lse(lse[bi], l_ref[j])
         assert torch.equal(kcd[1], kc[1]) and torch.equal(kcd[3], kc[3])  # rows no valid sequence uses
         with pytest.raises(RuntimeError, match="cache_batch_idx entries must be within cache batch bounds"):
             fai.flash_attn_kvcache_check(device)
@@ -160,6 +177,14 @@ def test_nosync_decode_step_in_hip_graph(device):
         graph.replay()
         torch.cuda.synchronize()
         kr, vr = kc_before.clone(), vc_before.clone()
+        # Each replay against the oracle (append + split-KV over the logical cache).
+        ok = [i for i, n in enumerate(lens) if n + 1 <= cap]
+        sel = torch.tensor(ok)
+        o_ref, l_ref, _, _ = kv_oracle(q.cpu()[sel], kc_before.cpu(), vc_before.cpu(), k.cpu()[sel], v.cpu()[sel],
+                                       torch.tensor(lens, dtype=torch.int32)[sel], None, tbl.cpu()[sel], True, 0, None)
+        for j, bi in enumerate(ok):
+            assert_2x(f"replay {i} out[{bi}]", out_g[bi].cpu(), o_ref[j], o_ref[j].to(torch.float16))
+            assert_lse(lse_g[bi].cpu(), l_ref[j])
         if max(lens) + 1 <= cap:
             out_r, lse_r = fai.flash_attn_with_kvcache(q, kr, vr, k, v, cache_seqlens=seqlens, **args)
             torch.cuda.synchronize()

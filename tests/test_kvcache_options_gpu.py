@@ -76,6 +76,15 @@ def test_kvcache_rotary(device, b, sq, h, hk, hd, cap, new, causal, splits, page
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_kvcache_rotary_column_sliced_tables(device, interleaved):
+    """cos / sin passed as column slices of wider tables (rows not packed): the
+    host layer hands the kernels packed copies, so the angles are the slices'."""
+    _check(device, 3, 2, 8, 2, 128, 1024, 2, True, 2, True, False, (-1, -1), 0.0, None, False,
+           rotary=(64, interleaved), sliced=True)
+
+
+@pytest.mark.gpu
 def test_kvcache_rotary_needs_new_keys(device):
     q = torch.zeros((1, 1, 4, 64), dtype=torch.float16, device=device)
     kc = torch.zeros((1, 256, 1, 64), dtype=torch.float16, device=device)
@@ -90,7 +99,7 @@ def test_kvcache_rotary_needs_new_keys(device):
 
 
 def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, window, softcap, alibi, leftpad,
-           rotary=None):
+           rotary=None, sliced=False):
     g = torch.Generator().manual_seed(8000 + b * 13 + sq + hd + cap // 256 + (alibi is not None) + 2 * leftpad
                                       + (0 if rotary is None else rotary[0]))
     rows = b + 2 if remap else b
@@ -112,6 +121,14 @@ def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, win
     if rotary is not None:
         ang = torch.rand((cap, rotary[0] // 2), generator=g, dtype=torch.float64) * 2 * torch.pi
         cos, sin = torch.cos(ang).to(torch.float16), torch.sin(ang).to(torch.float16)
+    cos_d = sin_d = None
+    if cos is not None:
+        cos_d, sin_d = cos.to(device), sin.to(device)
+        if sliced:  # the first rotary_dim / 2 columns of tables 16 columns wider
+            wide = torch.zeros((2, cap, rotary[0] // 2 + 16), dtype=torch.float16, device=device)
+            wide[0, :, : rotary[0] // 2], wide[1, :, : rotary[0] // 2] = cos_d, sin_d
+            cos_d, sin_d = wide[0, :, : rotary[0] // 2], wide[1, :, : rotary[0] // 2]
+            assert not cos_d.is_contiguous()
     table = None
     kcp, vcp = kc, vc
     if paged:
@@ -131,7 +148,7 @@ def _check(device, b, sq, h, hk, hd, cap, new, causal, splits, paged, remap, win
         window_size=window, softcap=softcap, return_softmax_lse=True,
         alibi_slopes=None if slopes is None else slopes.to(device),
         cache_leftpad=None if lpad is None else lpad.to(device),
-        rotary_cos=None if cos is None else cos.to(device), rotary_sin=None if sin is None else sin.to(device),
+        rotary_cos=cos_d, rotary_sin=sin_d,
         rotary_interleaved=True if rotary is None else rotary[1],
     )
     torch.cuda.synchronize()

@@ -447,3 +447,26 @@ def test_twin_rounds_where_the_reference_rounds():
     for a, b in zip(g_tw, g_ref):
         e = (a.float() - b).abs().max().item()
         assert 1e-5 < e < 2e-2
+
+
+def test_twin_error_matches_committed_fixture():
+    """The twin's error on the small committed cases equals tests/golden/ref_error.json:
+    a change to the twin's rounding points (an extra or a missing fp16 rounding)
+    moves these errors and fails here before it can move any GPU bound."""
+    import json
+    import os
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, os.path.join(here, "golden"))
+    import make_ref_error as mre
+
+    fx = json.load(open(os.path.join(here, "golden", "ref_error.json")))
+    for key in mre.SMALL:
+        err, noise = mre.small_case(key)
+        for n, e in err.items():
+            want = fx[key]["err_ref"][n]
+            assert abs(e - want) <= 0.05 * want, f"{key} {n}: twin error {e:.4e} vs committed {want:.4e}"
+        for n, z in noise.items():
+            want = fx[key]["noise_max"][n]
+            assert abs(z - want) <= 0.05 * want, f"{key} {n}: noise scale {z:.4e} vs committed {want:.4e}"

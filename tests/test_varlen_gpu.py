@@ -6,9 +6,7 @@ import pytest
 import torch
 
 import flash_attention_interface as fai
-from helpers import assert_2x, assert_lse, cu_from_lengths, randn16
-from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise
-from oracle.twin import bwd_twin, fwd_twin
+from helpers import check_varlen, cu_from_lengths, randn16
 
 CASES = [
     # lengths_q, lengths_k, h, hk, hd, causal
@@ -40,27 +38,7 @@ def test_varlen_parity(device, lens_q, lens_k, h, hk, hd, causal):
     )
     torch.cuda.synchronize()
     assert lse.shape == (len(lens_q), h, mq)
-    o_ref = torch.zeros(q.shape)
-    o_tw = torch.zeros(q.shape, dtype=torch.float16)
-    g_ref = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
-    g_tw = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
-    g_noise = [torch.zeros(q.shape), torch.zeros(k.shape), torch.zeros(v.shape)]
-    lse_ref = torch.zeros((len(lens_q), h, mq))
-    for b in range(len(lens_q)):
-        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
-        qb, kb, vb, dob = q[q0:q1][None], k[k0:k1][None], v[k0:k1][None], do[q0:q1][None]
-        ob, lb = attention_fwd(qb, kb, vb, s, causal)
-        otb, ltb = fwd_twin(qb, kb, vb, s, causal)
-        o_ref[q0:q1], o_tw[q0:q1], lse_ref[b, :, : q1 - q0] = ob[0], otb[0], lb[0]
-        gr = attention_bwd(qb, kb, vb, ob, lb, dob, s, causal)
-        gt = bwd_twin(qb, kb, vb, otb, ltb, dob, s, causal)
-        gn = bwd_fp32_noise(qb, kb, vb, ob, lb, dob, s, causal)
-        for i, (lo, hi) in enumerate([(q0, q1), (k0, k1), (k0, k1)]):
-            g_ref[i][lo:hi], g_tw[i][lo:hi], g_noise[i][lo:hi] = gr[i][0], gt[i][0].float(), gn[i][0]
-    assert_2x("out", out, o_ref, o_tw)
-    assert_lse(lse, lse_ref)  # includes the zero padding past each length
-    for name, got, r, t, n in zip(("dq", "dk", "dv"), (dq, dk, dv), g_ref, g_tw, g_noise):
-        assert_2x(name, got, r, t, n)
+    check_varlen("varlen", cu_q, cu_k, q, k, v, do, out.cpu(), lse.cpu(), (dq.cpu(), dk.cpu(), dv.cpu()), s, causal)
 
 
 @pytest.mark.gpu
@@ -75,6 +53,11 @@ def test_varlen_public_packed_variants(device):
     assert torch.equal(out_p, out)
     out_kv = fai.flash_attn_varlen_kvpacked_func(q, qkv[:, 1:], cu, cu, max(lens), max(lens), causal=True)
     assert torch.equal(out_kv, out)
+    # Against the oracle directly (the packed views are read in place).
+    qc, kc, vc = (t.cpu() for t in (q, k, v))
+    cuc = cu.cpu()
+    for tag, o in (("qkvpacked", out_p), ("kvpacked", out_kv)):
+        check_varlen(tag, cuc, cuc, qc, kc, vc, None, o.cpu(), None, None, 64 ** -0.5, True)
 
 
 @pytest.mark.gpu
@@ -98,3 +81,10 @@ def test_varlen_packed_bwd_matches_unpacked(device):
     fai.flash_attn_varlen_kvpacked_func(q2, kv, cu, cu, max(lens), max(lens), causal=True).backward(do)
     assert torch.equal(q2.grad, q.grad)
     assert torch.equal(kv.grad[:, 0], k.grad) and torch.equal(kv.grad[:, 1], v.grad)
+    # The packed gradients against the per-sequence oracle.
+    qc, kc, vc = (qkv.detach()[:, i].cpu() for i in range(3))
+    grads = tuple(qkv.grad[:, i].cpu() for i in range(3))
+    out = fai.flash_attn_varlen_qkvpacked_func(qkv.detach(), cu, max(lens), causal=True)
+    check_varlen("qkvpacked bwd", cu.cpu(), cu.cpu(), qc, kc, vc, do.cpu(), out.cpu(), None, grads, 64 ** -0.5, True)
+    kv_grads = (q2.grad.cpu(), kv.grad[:, 0].cpu(), kv.grad[:, 1].cpu())
+    check_varlen("kvpacked bwd", cu.cpu(), cu.cpu(), qc, kc, vc, do.cpu(), out.cpu(), None, kv_grads, 64 ** -0.5, True)
