@@ -3,6 +3,21 @@
 
 #include "fa_mi355x.h"
 
+namespace fa {
+// Compute units of the current device, queried once per device (launch shapes).
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+}  // namespace fa
+
 extern "C" int fa_check_tensor(const fa_tensor &t, bool required) {
     if (!t.ptr) return required ? FA_ERR_INVALID_ARG : FA_OK;
     if ((reinterpret_cast<uintptr_t>(t.ptr) & 15u) != 0) return FA_ERR_INVALID_ARG;

@@ -24,6 +24,9 @@
 
 namespace fa {
 
+// Compute units of the current device (host; fa_abi.hip).
+int device_cus();
+
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));

@@ -8,32 +8,41 @@
 // (fwd_kernel.h:415), O = 0 and LSE = 0 for a row with no visible key
 // (fwd_kernel.h:616-662).
 //
-// Design: one workgroup = 4 waves = 128 queries of one (batch, head); each
-// wave owns 32 queries.  The wave computes S^T = K Q^T (keys on the MFMA M
-// dimension) so each lane holds one query column and 32 keys of a 64-key
-// block: the row max needs one cross-half exchange and the row sum none.
-// Q^T stays in registers as the B operand.  K and V tiles go from HBM
-// straight into LDS with global_load_lds (no register staging), two stages,
-// the next block's copy in flight while the current block is computed; V is
-// kept in its natural layout and read transposed with ds_read_b64_tr_b16.
-// P^T feeds the O^T += V^T P^T MFMAs directly from the accumulators (see
-// fa_common.h).  Two workgroups share a CU (64 KB LDS each at head_dim 128),
-// so one wave's softmax overlaps the other's MFMAs on each SIMD.
+// Each wave owns 32 queries of one (batch, head) and walks 64-key blocks.  It
+// computes S^T = K Q^T (keys on the MFMA M dimension) so each lane holds one
+// query column and 32 keys of a block: the row max needs one cross-half
+// exchange and the row sum none.  Q^T stays in registers as the B operand.  K
+// and V tiles go from HBM straight into LDS with global_load_lds (no register
+// staging), two stages; V keeps its natural layout and is read transposed
+// with ds_read_b64_tr_b16.  P^T feeds the O^T += V^T P^T MFMAs directly from
+// the accumulators (see fa_common.h).
+//
+// Two kernels share that per-wave arithmetic (so their results are the same
+// bit for bit) and differ in how the waves of a SIMD take turns:
+//   * fwd_pp_kernel (head_dim 128, grids of at least two workgroups per CU):
+//     8 waves, two per SIMD, in two groups that alternate a matrix phase (the
+//     PV product of block j - 1 and the S product of block j: all the LDS
+//     operand reads and MFMAs) and a softmax phase (block j's exponentials),
+//     separated by workgroup barriers, so one group's softmax runs on the
+//     VALU while the other group's MFMAs run on the matrix cores;
+//   * fwd_kernel (head_dim 64 and small grids): 4 waves, two independent
+//     workgroups per CU.
 #include <type_traits>
 
 #include "fa_common.h"
 
+#define FA_INLINE __attribute__((always_inline))
+
 namespace fa {
 
-template <int HD>
+constexpr int kFwdBN = 64;  // keys per block
+
+template <int HD, int NT>
 struct FwdCfg {
-    static constexpr int NT = 256;                // threads
-    static constexpr int OCC = 2;                 // workgroups per CU
     static constexpr int BM = 32 * (NT / 64);     // queries per workgroup (32 per wave)
-    static constexpr int BN = 64;                 // keys per block
-    static constexpr int KCH = HD / 8;            // 16-byte chunks per row
+    static constexpr int BN = kFwdBN;
     static constexpr int TILE = BN * HD * 2;      // one K or V tile
-    static constexpr int STAGE = 2 * TILE;        // K tile, then V tile
+    static constexpr int STAGE = 2 * TILE;        // a K tile and a V tile
 };
 
 // The running maximum m a row's probabilities P = exp2(S*c - m) are taken
@@ -57,189 +66,145 @@ __device__ __forceinline__ float sum8(const f16x8 &v, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
 }
 
-template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
-    using C = FwdCfg<HD>;
-    constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
-    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+// Per-workgroup extents and base pointers of one (batch, head, query block).
+struct FwdWork {
+    int b, h, hk, sq, sk, m0, causal_off, n_blocks;
+    const f16 *qp, *kp, *vp;
+    f16 *op;
+    float *lse_row;
+    float cscale;
+    bool neg;
+};
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-    const int col = lane & 31, hh = lane >> 5;
-
-    // Causal blocks are issued heaviest (largest m block) first.
+// Fills w for workgroup blockIdx.x; false when the block has no query rows
+// (its LSE padding is then written here).
+template <int BM, bool CAUSAL>
+__device__ __forceinline__ bool fwd_work(const fa_fwd_args &a, int num_m_blocks, FwdWork &w) {
     const int bh_count = a.batch * a.nheads;
     const int bh = blockIdx.x % bh_count;
     int mb = blockIdx.x / bh_count;
-    if (CAUSAL) mb = num_m_blocks - 1 - mb;
-    const int b = bh / a.nheads, h = bh - b * a.nheads;
-    const int hk = h / (a.nheads / a.nheads_k);
-
+    if (CAUSAL) mb = num_m_blocks - 1 - mb;  // causal blocks are issued heaviest first
+    w.b = bh / a.nheads;
+    w.h = bh - w.b * a.nheads;
+    w.hk = w.h / (a.nheads / a.nheads_k);
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
-    const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k,
+    const SeqInfo si = seq_info(w.b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k,
                                 a.seqused_k_add);
-    const int sq = si.sq;
-    int sk = si.sk;
-    int kb = a.k_batch_idx ? a.k_batch_idx[b] : b;
+    w.sq = si.sq;
+    w.sk = si.sk;
+    int kb = a.k_batch_idx ? a.k_batch_idx[w.b] : w.b;
     if (a.seqused_k) {
         // KV-cache chunk: a key count past the cache or a cache row outside it
         // leaves the batch with no keys, and the error goes to the status word.
-        const int used = a.seqused_k[b];
+        const int used = a.seqused_k[w.b];
         const int err = (used < 0 || int64_t(used) + a.seqused_k_add > a.seqlen_k ? 1 : 0) |
                         (a.k_batch_idx && a.k_batch > 0 && (kb < 0 || kb >= a.k_batch) ? 2 : 0);
         if (err) {
-            sk = 0;
+            w.sk = 0;
             kb = 0;
-            if (a.status && tid == 0) atomicOr(a.status, err);
+            if (a.status && threadIdx.x == 0) atomicOr(a.status, err);
         }
     }
-    const int m0 = mb * BM;
-    float *lse_row = a.lse + (int64_t(b) * a.nheads + h) * a.lse_seqlen;
-    if (m0 >= sq) {
+    w.m0 = mb * BM;
+    w.lse_row = a.lse + (int64_t(w.b) * a.nheads + w.h) * a.lse_seqlen;
+    if (w.m0 >= w.sq) {
         // Rows past this sequence's length: LSE padding is 0 (flash_api.cpp:388).
-        for (int i = m0 + tid; i < m0 + BM && i < a.lse_seqlen; i += NT) lse_row[i] = 0.f;
-        return;
+        for (int i = w.m0 + threadIdx.x; i < w.m0 + BM && i < a.lse_seqlen; i += blockDim.x) w.lse_row[i] = 0.f;
+        return false;
     }
-    const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, h);
-    const f16 *kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, kb, si.k_start, hk);
-    const f16 *vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, kb, si.k_start, hk);
-    f16 *op = (f16 *)a.o.ptr + base_off(a.o, packed_q, b, si.q_start, h);
-    const int64_t qrs = a.q.row_stride, krs = a.k.row_stride, vrs = a.v.row_stride, ors = a.o.row_stride;
-
-    const int causal_off = sk - sq;  // key j visible to query i iff j <= i + causal_off
-    int n_end = sk;
-    if (CAUSAL) n_end = max(0, min(sk, m0 + BM + causal_off));
-    const int n_blocks = (n_end + BN - 1) / BN;
-
+    w.qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, w.b, si.q_start, w.h);
+    w.kp = (const f16 *)a.k.ptr + base_off(a.k, packed_k, kb, si.k_start, w.hk);
+    w.vp = (const f16 *)a.v.ptr + base_off(a.v, packed_k, kb, si.k_start, w.hk);
+    w.op = (f16 *)a.o.ptr + base_off(a.o, packed_q, w.b, si.q_start, w.h);
+    w.causal_off = w.sk - w.sq;  // key j visible to query i iff j <= i + causal_off
+    int n_end = w.sk;
+    if (CAUSAL) n_end = max(0, min(w.sk, w.m0 + BM + w.causal_off));
+    w.n_blocks = (n_end + kFwdBN - 1) / kFwdBN;
     // Negative scales are folded into Q's sign so that the exp argument uses |scale|.
-    const bool neg = a.softmax_scale < 0.f;
-    const float cscale = fabsf(a.softmax_scale) * kLog2e;
+    w.neg = a.softmax_scale < 0.f;
+    w.cscale = fabsf(a.softmax_scale) * kLog2e;
+    return true;
+}
 
-    // Q^T as the B operand: lane (query col, half hh), K step g covers d = 16g + 8hh + 0..7.
-    const int qi = m0 + wave * 32 + col;
-    f16x8 qB[HD / 16];
+// Q^T of query qi as B operands: lane (query col, half hh), K step g covers d = 16g + 8hh + 0..7.
+template <int HD>
+__device__ __forceinline__ void load_q(const fa_fwd_args &a, const FwdWork &w, int qi, int hh, f16x8 (&qB)[HD / 16]) {
 #pragma unroll
     for (int g = 0; g < HD / 16; ++g) {
         u32x4 v = zero_u4();
-        if (qi < sq) v = ldg16(qp + int64_t(qi) * qrs + 16 * g + 8 * hh);
-        if (neg) v = neg_h8(v);
+        if (qi < w.sq) v = ldg16(w.qp + int64_t(qi) * a.q.row_stride + 16 * g + 8 * hh);
+        if (w.neg) v = neg_h8(v);
         qB[g] = as_h8(v);
     }
-    wait_vmem();  // only the tile copies are in flight inside the loop
+}
 
-    f32x16 o[HD / 32];
-#pragma unroll
-    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
+// Online-softmax state of a wave's 32 queries (this lane's query column).
+struct SoftmaxRow {
     float m_t = -INFINITY;  // reference max of scale*log2(e)*S for this lane's query
     float l_p = 0.f;        // partial row sum over this lane half's keys (fp32 P, for the LSE)
     float l_o = 0.f;        // the same over the fp16-rounded P (normalises O)
+};
 
-    TileReader<HD> rd;
-    rd.init(lane);
-    TileCopier<HD, BN, NT> kcp, vcp;
-    kcp.init(krs, wave, lane);
-    vcp.init(vrs, wave, lane);
-    // Copy of key block nb into stage st.  A block that runs past the
-    // sequence re-reads its last key for the missing rows (masked below).
-    const uint32_t smem_l = lds_addr(smem);
-    auto issue = [&](int nb, int st) {
-        char *ks = smem + st * C::STAGE;
-        const int n0 = nb * BN;
-        if (n0 + BN <= sk) {
-            kcp.copy_to(smem_l + st * C::STAGE, kp + int64_t(n0) * krs, krs);
-            vcp.copy_to(smem_l + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
-        } else {
-            dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
-            dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
-        }
-    };
-
-    const int q_lo = m0 + wave * 32;
-    // One key block: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASK is a
-    // compile-time switch so the blocks away from the causal diagonal and
-    // the sequence end carry no masking work at all.
-    auto block = [&](int nb, auto mask_tag) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        const int buf = nb & 1;
-        wait_vmem();
-        __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
-        if (nb + 1 < n_blocks) issue(nb + 1, buf ^ 1);
-        const int n0 = nb * BN;
-        if (CAUSAL && MASK && n0 > q_lo + 31 + causal_off) return;  // no visible key for this wave
-        const char *ks = smem + buf * C::STAGE;
-        const char *vs = ks + C::TILE;
-        f32x16 s[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
-#pragma unroll
-            for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
-        }
-        if constexpr (MASK) {
-            const int lim = (CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1) - n0;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (kt * 32 + acc_lrow(r, hh) > lim) s[kt][r] = -INFINITY;
-        }
-        float mx = s[0][0];
+// One 64-key block of S^T (two 32 x 32 accumulator tiles) -> P^T operands:
+// mask (MASK: keys past lim, relative to the block start), running maximum,
+// lazy rescale of O, exponentials, row sums.
+template <int HD, bool MASK>
+__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f32x16 (&o)[HD / 32], SoftmaxRow &r,
+                                              float cscale, int lim, int hh) {
+    if constexpr (MASK) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-        mx = max_xor32(mx);
-        const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
-        if (__builtin_amdgcn_ballot_w64(mx_t > m_t + kRescaleSlack) != 0) {
-            const float m_new = fmaxf(m_t, mx_t);
-            const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_t - m_new);
-            l_p *= alpha;
-            l_o *= alpha;
+            for (int e = 0; e < 16; ++e)
+                if (kt * 32 + acc_lrow(e, hh) > lim) s[kt][e] = -INFINITY;
+    }
+    float mx = s[0][0];
 #pragma unroll
-            for (int dt = 0; dt < HD / 32; ++dt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-            m_t = m_new;
-        }
-        const float m_use = m_t == -INFINITY ? 0.f : m_t;
-        float rs = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float x = s[kt][r];
-                float p = exp2_fast(fmaf(x, cscale, -m_use));
-                if constexpr (MASK) p = x == -INFINITY ? 0.f : p;
-                s[kt][r] = p;
-                rs += p;
-            }
-        l_p += rs;
-        f16x8 pB[4];
-#pragma unroll
-        for (int gg = 0; gg < 4; ++gg) {
-            pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
-            l_o = sum8(pB[gg], l_o);
-        }
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
+    mx = max_xor32(mx);
+    const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
+    if (__builtin_amdgcn_ballot_w64(mx_t > r.m_t + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(r.m_t, mx_t);
+        const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(r.m_t - m_new);
+        r.l_p *= alpha;
+        r.l_o *= alpha;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(rd.tr_operand(vs, 16 * gg, dt), pB[gg], o[dt]);
-    };
+            for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+        r.m_t = m_new;
+    }
+    const float m_use = r.m_t == -INFINITY ? 0.f : r.m_t;
+    float rs = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float x = s[kt][e];
+            float p = exp2_fast(fmaf(x, cscale, -m_use));
+            if constexpr (MASK) p = x == -INFINITY ? 0.f : p;
+            s[kt][e] = p;
+            rs += p;
+        }
+    r.l_p += rs;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+        pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+        r.l_o = sum8(pB[gg], r.l_o);
+    }
+}
 
-    // Blocks [0, n_full) need no mask for any wave of the workgroup: every key
-    // is below the sequence end and at or below the diagonal of the first query.
-    int n_full = min(n_blocks, sk / BN);
-    if (CAUSAL) n_full = min(n_full, max(0, (m0 + causal_off + 1) / BN));
-    if (n_blocks > 0) issue(0, 0);
-    for (int nb = 0; nb < n_full; ++nb) block(nb, std::false_type{});
-    for (int nb = n_full; nb < n_blocks; ++nb) block(nb, std::true_type{});
-
-    // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
-    const float l_tot = sum_xor32(l_p);
-    const float lo_tot = sum_xor32(l_o);
-    if (qi < sq) {
+// Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
+template <int HD>
+__device__ __forceinline__ void store_row(const fa_fwd_args &a, const FwdWork &w, int qi, int hh,
+                                          const f32x16 (&o)[HD / 32], const SoftmaxRow &r) {
+    const float l_tot = sum_xor32(r.l_p);
+    const float lo_tot = sum_xor32(r.l_o);
+    if (qi < w.sq) {
         const float inv = lo_tot > 0.f ? 1.f / lo_tot : 0.f;
-        f16 *orow = op + int64_t(qi) * ors;
+        f16 *orow = w.op + int64_t(qi) * a.o.row_stride;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
@@ -249,20 +214,304 @@ __global__ __launch_bounds__(FwdCfg<HD>::NT, FwdCfg<HD>::OCC) void fwd_kernel(co
                 for (int t = 0; t < 4; ++t) v[t] = (f16)(o[dt][4 * a4 + t] * inv);
                 *reinterpret_cast<f16x4 *>(orow + dt * 32 + 8 * a4 + 4 * hh) = v;
             }
-        if (hh == 0) lse_row[qi] = l_tot > 0.f ? (m_t + log2_fast(l_tot)) * kLn2 : 0.f;
+        if (hh == 0) w.lse_row[qi] = l_tot > 0.f ? (r.m_t + log2_fast(l_tot)) * kLn2 : 0.f;
     } else if (hh == 0 && qi < a.lse_seqlen) {
-        lse_row[qi] = 0.f;
+        w.lse_row[qi] = 0.f;
     }
+}
+
+// Copies of K / V block nb into an LDS tile by all NT threads.  A block that
+// runs past the sequence re-reads its last key for the missing rows (masked).
+template <int HD, int NT>
+struct KvLoader {
+    TileCopier<HD, kFwdBN, NT> kcp, vcp;
+    __device__ __forceinline__ void init(const fa_fwd_args &a, int wave, int lane) {
+        kcp.init(a.k.row_stride, wave, lane);
+        vcp.init(a.v.row_stride, wave, lane);
+    }
+    __device__ __forceinline__ void k(const fa_fwd_args &a, const FwdWork &w, char *smem, uint32_t off, int nb,
+                                      int wave, int lane) const {
+        const int n0 = nb * kFwdBN;
+        if (n0 + kFwdBN <= w.sk)
+            kcp.copy_to(lds_addr(smem) + off, w.kp + int64_t(n0) * a.k.row_stride, a.k.row_stride);
+        else
+            dma_tile<HD, kFwdBN, NT>(smem + off, w.kp, a.k.row_stride, n0, w.sk - 1, wave, lane);
+    }
+    __device__ __forceinline__ void v(const fa_fwd_args &a, const FwdWork &w, char *smem, uint32_t off, int nb,
+                                      int wave, int lane) const {
+        const int n0 = nb * kFwdBN;
+        if (n0 + kFwdBN <= w.sk)
+            vcp.copy_to(lds_addr(smem) + off, w.vp + int64_t(n0) * a.v.row_stride, a.v.row_stride);
+        else
+            dma_tile<HD, kFwdBN, NT>(smem + off, w.vp, a.v.row_stride, n0, w.sk - 1, wave, lane);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// 4-wave kernel: each wave runs S, softmax and PV of a block in turn; two
+// workgroups per CU (64 KB LDS each at head_dim 128) overlap one wave's
+// softmax with the other's MFMAs on each SIMD.
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
+    constexpr int NT = 256;
+    using C = FwdCfg<HD, NT>;
+    constexpr int BM = C::BM, BN = C::BN;
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int hh = lane >> 5;
+    FwdWork w;
+    if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, w)) return;
+
+    const int q_lo = w.m0 + wave * 32;
+    const int qi = q_lo + (lane & 31);
+    f16x8 qB[HD / 16];
+    load_q<HD>(a, w, qi, hh, qB);
+    wait_vmem();  // only the tile copies are in flight inside the loop
+
+    f32x16 o[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
+    SoftmaxRow row;
+
+    TileReader<HD> rd;
+    rd.init(lane);
+    KvLoader<HD, NT> ld;
+    ld.init(a, wave, lane);
+    auto issue = [&](int nb, int st) FA_INLINE {
+        ld.k(a, w, smem, st * C::STAGE, nb, wave, lane);
+        ld.v(a, w, smem, st * C::STAGE + C::TILE, nb, wave, lane);
+    };
+
+    // One key block: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASK is a
+    // compile-time switch so the blocks away from the causal diagonal and
+    // the sequence end carry no masking work at all.
+    auto block = [&](int nb, auto mask_tag) FA_INLINE {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int buf = nb & 1;
+        wait_vmem();
+        __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
+        if (nb + 1 < w.n_blocks) issue(nb + 1, buf ^ 1);
+        const int n0 = nb * BN;
+        if (CAUSAL && MASK && n0 > q_lo + 31 + w.causal_off) return;  // no visible key for this wave
+        const char *ks = smem + buf * C::STAGE;
+        const char *vs = ks + C::TILE;
+        f32x16 s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
+#pragma unroll
+            for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
+        }
+        const int lim = (CAUSAL ? min(w.sk - 1, qi + w.causal_off) : w.sk - 1) - n0;
+        f16x8 pB[4];
+        softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(rd.tr_operand(vs, 16 * gg, dt), pB[gg], o[dt]);
+    };
+
+    // Blocks [0, n_full) need no mask for any wave of the workgroup: every key
+    // is below the sequence end and at or below the diagonal of the first query.
+    int n_full = min(w.n_blocks, w.sk / BN);
+    if (CAUSAL) n_full = min(n_full, max(0, (w.m0 + w.causal_off + 1) / BN));
+    if (w.n_blocks > 0) issue(0, 0);
+    for (int nb = 0; nb < n_full; ++nb) block(nb, std::false_type{});
+    for (int nb = n_full; nb < w.n_blocks; ++nb) block(nb, std::true_type{});
+    store_row<HD>(a, w, qi, hh, o, row);
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong kernel: 8 waves over 256 queries.  Waves w and w + 4 share a SIMD
+// (waves go to the SIMDs in order, 0..3 then again 0..3); group g = w / 4
+// holds 32-query tile 2 (w % 4) + g, so both groups span the workgroup's rows
+// and reach the causal diagonal together.  Iteration j (two barriers):
+//   group 0: matrix phase [PV of block j - 1, S of block j] | softmax of j
+//   group 1: softmax of j - 1 | matrix phase [PV of j - 1, S of j]
+// Stage j & 1 holds K_j and V_{j - 1}; the next stage's copies (K_{j + 1},
+// V_j) go out at the start of iteration j.  Matrix-phase operands are read
+// PIPE steps ahead of their MFMAs with a scheduling fence per step.
+constexpr int kPpPipe = 8;
+
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, const int num_m_blocks) {
+    constexpr int NT = 512;
+    using C = FwdCfg<HD, NT>;
+    constexpr int BM = C::BM, BN = C::BN;
+    __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int grp = wave >> 2;                                  // 0: matrix phase first
+    const int hh = lane >> 5;
+    FwdWork w;
+    if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, w)) return;
+
+    const int q_lo = w.m0 + (2 * (wave & 3) + grp) * 32;
+    const int qi = q_lo + (lane & 31);
+    f16x8 qB[HD / 16];
+    load_q<HD>(a, w, qi, hh, qB);
+    wait_vmem();  // only the tile copies are in flight inside the loop
+
+    f32x16 o[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
+    SoftmaxRow row;
+
+    TileReader<HD> rd;
+    rd.init(lane);
+    KvLoader<HD, NT> ld;
+    ld.init(a, wave, lane);
+
+    // Last key this wave sees; blocks [0, nbw) hold its keys, and blocks
+    // [0, n_full) need no mask for any of its queries.
+    const int wave_last_key = CAUSAL ? min(w.sk - 1, q_lo + 31 + w.causal_off) : w.sk - 1;
+    const int nbw = max(0, min(w.n_blocks, (wave_last_key + BN) / BN));
+    int n_full = min(w.n_blocks, w.sk / BN);
+    if (CAUSAL) n_full = min(n_full, max(0, (q_lo + w.causal_off + 1) / BN));
+
+    f32x16 s[2];
+    f16x8 pB[4];
+    // Matrix phase of iteration j: O^T += V_{j-1}^T P_{j-1}^T (DO_PV), then
+    // S_j^T = K_j Q^T (DO_S); step t < NPV is a PV MFMA, the rest S MFMAs.
+    constexpr int NPV = 4 * (HD / 32), NS = 2 * (HD / 16);
+    auto matrix = [&](int j, auto pv_tag, auto s_tag) FA_INLINE {
+        constexpr bool DO_PV = decltype(pv_tag)::value, DO_S = decltype(s_tag)::value;
+        constexpr int T0 = DO_PV ? 0 : NPV, T1 = DO_S ? NPV + NS : NPV;
+        const char *ks = smem + (j & 1) * C::STAGE;
+        const char *vs = ks + C::TILE;
+        // The per-read LDS addresses are recomputed from an opaque copy of the
+        // lane's base offsets: hoisted out of the loop they would hold
+        // registers for the whole kernel.
+        TileReader<HD> r = rd;
+        asm volatile("" : "+v"(r.a_base), "+v"(r.tr_base[0]), "+v"(r.tr_base[1]));
+        f16x8 opnd[kPpPipe];
+        auto read = [&](int t) FA_INLINE {
+            if (t < NPV)
+                opnd[t % kPpPipe] = r.tr_operand(vs, 16 * (t & 3), t >> 2);
+            else
+                opnd[t % kPpPipe] = r.a_operand(ks, 32 * ((t - NPV) / (HD / 16)), (t - NPV) % (HD / 16));
+        };
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = T0; t < T0 + kPpPipe - 1 && t < T1; ++t) read(t);
+#pragma unroll
+        for (int t = T0; t < T1; ++t) {
+            if (t + kPpPipe - 1 < T1) read(t + kPpPipe - 1);
+            if (t < NPV) {
+                o[t >> 2] = mfma32(opnd[t % kPpPipe], pB[t & 3], o[t >> 2]);
+            } else {
+                const int u = t - NPV, kt = u / (HD / 16), g = u % (HD / 16);
+                s[kt] = mfma32(opnd[t % kPpPipe], qB[g], g == 0 ? zero16() : s[kt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto softmax = [&](int j, auto mask_tag) FA_INLINE {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int lim = (CAUSAL ? min(w.sk - 1, qi + w.causal_off) : w.sk - 1) - j * BN;
+        softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
+    };
+    auto softmax_any = [&](int j) FA_INLINE {
+        if (j < n_full)
+            softmax(j, std::false_type{});
+        else
+            softmax(j, std::true_type{});
+    };
+    // Start of iteration j: K_j and V_{j-1} are in stage j & 1 (every wave's
+    // copies have landed) and stage (j + 1) & 1 is free: the next copies go out.
+    auto top = [&](int j) FA_INLINE {
+        wait_vmem();
+        __syncthreads();
+        if (j < w.n_blocks) {
+            if (j + 1 < w.n_blocks) ld.k(a, w, smem, ((j + 1) & 1) * C::STAGE, j + 1, wave, lane);
+            ld.v(a, w, smem, ((j + 1) & 1) * C::STAGE + C::TILE, j, wave, lane);
+        }
+    };
+    auto mid = []() FA_INLINE { __builtin_amdgcn_s_barrier(); };
+    using T = std::true_type;
+    using F = std::false_type;
+
+    // Every wave runs iterations 0..n_blocks (two barriers each); a wave does
+    // S for blocks j < nbw and PV for 1 <= j <= nbw.
+    if (w.n_blocks > 0) ld.k(a, w, smem, 0, 0, wave, lane);
+    int j = 1;
+    if (grp == 0) {
+        top(0);
+        if (nbw > 0) matrix(0, F{}, T{});
+        mid();
+        if (nbw > 0) softmax_any(0);
+        for (; j < min(nbw, n_full); ++j) {
+            top(j);
+            matrix(j, T{}, T{});
+            mid();
+            softmax(j, F{});
+        }
+        for (; j < nbw; ++j) {
+            top(j);
+            matrix(j, T{}, T{});
+            mid();
+            softmax(j, T{});
+        }
+        if (nbw > 0) {
+            top(nbw);
+            matrix(nbw, T{}, F{});
+            mid();
+            j = nbw + 1;
+        }
+    } else {
+        top(0);
+        mid();
+        if (nbw > 0) matrix(0, F{}, T{});
+        for (; j < min(nbw, n_full + 1); ++j) {
+            top(j);
+            softmax(j - 1, F{});
+            mid();
+            matrix(j, T{}, T{});
+        }
+        for (; j < nbw; ++j) {
+            top(j);
+            softmax(j - 1, T{});
+            mid();
+            matrix(j, T{}, T{});
+        }
+        if (nbw > 0) {
+            top(nbw);
+            softmax_any(nbw - 1);
+            mid();
+            matrix(nbw, T{}, F{});
+            j = nbw + 1;
+        }
+    }
+    for (; j <= w.n_blocks; ++j) {
+        top(j);
+        mid();
+    }
+    store_row<HD>(a, w, qi, hh, o, row);
 }
 
 template <int HD, bool CAUSAL>
 static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
-    const int num_m_blocks = (a.lse_seqlen + FwdCfg<HD>::BM - 1) / FwdCfg<HD>::BM;
+    // The ping-pong kernel when its grid fills the chip at least twice over;
+    // the 4-wave kernel otherwise (and at head_dim 64, where it measured
+    // faster).  Both give the same bits.
+    if constexpr (HD == 128) {
+        const int64_t pp_m_blocks = (a.lse_seqlen + FwdCfg<HD, 512>::BM - 1) / FwdCfg<HD, 512>::BM;
+        const int64_t pp_grid = pp_m_blocks * a.batch * a.nheads;
+        if (pp_grid >= 2 * int64_t(device_cus())) {
+            if (pp_grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+            hipLaunchKernelGGL((fwd_pp_kernel<HD, CAUSAL>), dim3(unsigned(pp_grid)), dim3(512), 0, stream, a,
+                               int(pp_m_blocks));
+            return int(hipGetLastError());
+        }
+    }
+    const int num_m_blocks = (a.lse_seqlen + FwdCfg<HD, 256>::BM - 1) / FwdCfg<HD, 256>::BM;
     const int64_t grid = int64_t(num_m_blocks) * a.batch * a.nheads;
     if (grid == 0) return FA_OK;
     if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
-    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(FwdCfg<HD>::NT), 0, stream, a,
-                       num_m_blocks);
+    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(256), 0, stream, a, num_m_blocks);
     return int(hipGetLastError());
 }
 

@@ -599,19 +599,6 @@ __global__ __launch_bounds__(256) void kv_combine_kernel(const fa_kvcache_args a
     if (lane == 0) a.lse[r] = live ? ltot : 0.f;
 }
 
-// Compute units of the current device, queried once per device.
-static int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 static int check_kv(const fa_kvcache_args *p) {
     if (!p) return FA_ERR_INVALID_ARG;
     const fa_kvcache_args &a = *p;
