@@ -35,6 +35,9 @@ extern "C" const char *fa_error_string(int code) {
             return "fa_mi355x: unsupported configuration (head_dim must be 64 or 128)";
         case FA_ERR_WORKSPACE:
             return "fa_mi355x: missing or too small workspace";
+        case FA_ERR_SCRATCH:
+            return "fa_mi355x: request needs more than the 16 MiB static scratch of fa_fwd_kvcache_noalloc "
+                   "(fewer splits or a smaller batch, or fa_fwd_kvcache with a caller workspace)";
         default:
             return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "fa_mi355x: unknown error";
     }

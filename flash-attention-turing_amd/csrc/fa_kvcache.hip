@@ -32,6 +32,7 @@
 // device counter in that order, so the longest sequences start first, the
 // short ones fill the end, and no workgroup is relaunched between items.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "fa_common.h"
@@ -738,4 +739,67 @@ extern "C" int fa_fwd_kvcache(const fa_kvcache_args *args, void *stream) {
     rc = fa_kv_splitkv(args, stream);
     if (rc) return rc;
     return fa_kv_combine(args, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: fa_fwd_kvcache with its split workspace (out_accum,
+// lse_accum, batch_order) carved from a static device array instead of
+// caller memory, for callers that cannot allocate (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc).  The array is
+// FA_NOALLOC_SCRATCH_BYTES per device for the life of the process; its device
+// address is looked up once per device (hipGetSymbolAddress) and only that
+// address is handed to the kernels.  Nothing in it needs clearing between
+// calls: the split kernel writes every partial it later combines, and the
+// ordering kernel resets the work counter.  Calls on one device share the
+// array, so calls that overlap on a device (different streams) race.
+static __device__ __align__(256) char scratch[FA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices] = {};
+
+// Device address of this device's scratch array (looked up on the device's first call).
+int scratch_address(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return int(e);
+    if (dev < 0 || dev >= kMaxDevices) return FA_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return int(e);
+        if (!p) return FA_ERR_SCRATCH;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return FA_OK;
+}
+
+// Scratch bytes a call needs: the split accumulators, then batch + 1 int32s of order and counter.
+size_t noalloc_bytes(const fa_kvcache_args *a) {
+    return fa_kv_workspace_bytes(a) + (size_t(a->batch > 0 ? a->batch : 0) + 1) * sizeof(int32_t);
+}
+
+}  // namespace
+
+extern "C" int fa_fwd_kvcache_noalloc(const fa_kvcache_args *args, void *stream) {
+    int rc = fa::check_kv(args);
+    if (rc) return rc;
+    if (noalloc_bytes(args) > FA_NOALLOC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+    void *base = nullptr;
+    if ((rc = scratch_address(&base))) return rc;
+    fa_kvcache_args a = *args;
+    const size_t acc = fa_kv_workspace_bytes(&a);
+    float *f = static_cast<float *>(base);
+    if (a.num_splits > 1) {
+        a.out_accum = f;
+        a.lse_accum = f + size_t(a.num_splits) * a.batch * a.nheads * a.seqlen_q * a.head_dim;
+    } else {
+        a.out_accum = a.lse_accum = nullptr;
+    }
+    a.batch_order = reinterpret_cast<int32_t *>(static_cast<char *>(base) + acc);
+    return fa_fwd_kvcache(&a, stream);
 }

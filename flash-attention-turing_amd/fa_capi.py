@@ -22,6 +22,7 @@ FA_OK = 0
 FA_ERR_INVALID_ARG = -1
 FA_ERR_UNSUPPORTED = -2
 FA_ERR_WORKSPACE = -3
+FA_ERR_SCRATCH = -4
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -81,6 +82,7 @@ _ARGP = {
     "fa_kv_splitkv": FaKvcacheArgs,
     "fa_kv_combine": FaKvcacheArgs,
     "fa_fwd_kvcache": FaKvcacheArgs,
+    "fa_fwd_kvcache_noalloc": FaKvcacheArgs,
 }
 
 _lib = None

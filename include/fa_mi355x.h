@@ -31,7 +31,8 @@ enum {
     FA_OK = 0,
     FA_ERR_INVALID_ARG = -1,   /* shape / pointer / alignment check failed   */
     FA_ERR_UNSUPPORTED = -2,   /* head_dim not in {64, 128} and similar      */
-    FA_ERR_WORKSPACE = -3      /* missing or too small workspace             */
+    FA_ERR_WORKSPACE = -3,     /* missing or too small workspace             */
+    FA_ERR_SCRATCH = -4        /* request beyond fa_fwd_kvcache_noalloc's static scratch */
     /* positive values are hipError_t codes from the launch                  */
 };
 
@@ -192,6 +193,21 @@ int fa_kv_splitkv(const fa_kvcache_args *args, void *stream);
 int fa_kv_combine(const fa_kvcache_args *args, void *stream);
 /* append + split-KV + combine in stream order. */
 int fa_fwd_kvcache(const fa_kvcache_args *args, void *stream);
+
+/*
+ * Allocation-free variant of fa_fwd_kvcache.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * same kernels run; out_accum, lse_accum and batch_order in args are ignored
+ * and taken instead from a static device array of FA_NOALLOC_SCRATCH_BYTES per
+ * device, held until the process ends (the calling thread's current device
+ * must be the stream's).  A request needing more than that, i.e.
+ * fa_kv_workspace_bytes(args) + 4 * (batch + 1) bytes, returns FA_ERR_SCRATCH.
+ * No allocation or free happens in the call.  Calls on one device share its
+ * array: calls that overlap on one device (on different streams) race.
+ */
+#define FA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int fa_fwd_kvcache_noalloc(const fa_kvcache_args *args, void *stream);
 
 /* Human-readable text for a return code (FA_* or hipError_t). */
 const char *fa_error_string(int code);
