@@ -101,7 +101,7 @@ class Timed:
         return wall * 1e3 / steps, per
 
 
-def train_step_setup(batch, seqlen, heads, hd, seed, device):
+def train_step_setup(batch, seqlen, heads, hd, seed, device, causal=True):
     import torch
 
     import fa_capi
@@ -114,8 +114,8 @@ def train_step_setup(batch, seqlen, heads, hd, seed, device):
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=device)  # -D, LSE*log2(e)
     scale = hd ** -0.5
-    fa = fa_capi.fwd_args(q, k, v, o, lse, scale, True)
-    ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, True)
+    fa = fa_capi.fwd_args(q, k, v, o, lse, scale, causal)
+    ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, causal)
     # fa_bwd_dq also computes D = rowsum(dO * O) (the preprocess) for fa_bwd_dkdv.
     launches = [
         ("fwd", lambda: fa_capi.call("fa_fwd", fa)),
@@ -126,8 +126,8 @@ def train_step_setup(batch, seqlen, heads, hd, seed, device):
     return launches, tensors
 
 
-def train_report(batch, seqlen, heads, hd, ms_step, per):
-    pairs = causal_pairs(seqlen, seqlen)
+def train_report(batch, seqlen, heads, hd, ms_step, per, causal=True):
+    pairs = causal_pairs(seqlen, seqlen) if causal else seqlen * seqlen
     unit = batch * heads * hd * pairs
     flops = {"fwd": 4 * unit, "bwd_dq": 6 * unit, "bwd_dkdv": 8 * unit}
     kern = {}
@@ -283,11 +283,44 @@ def longctx_setup(device, seed=4):
     return launches, info, dict(out=out)
 
 
+def _cpu_threads():
+    """The host cores this process may run on (the GPU box's share), used for every CPU leg."""
+    import torch
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    return n
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, min_runs=5, min_seconds=10.0, max_runs=60):
+    """One warm-up call, then at least min_runs timed calls and at least min_seconds of them."""
+    fn()
+    times = []
+    t_all = time.perf_counter()
+    while len(times) < max_runs and (len(times) < min_runs or time.perf_counter() - t_all < min_seconds):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline_train(tensors, hd):
-    """CPU SDPA fwd + bwd (fp32, causal) on batch 1 of the headline inputs."""
+    """CPU SDPA fwd + bwd (fp32, causal) on batch row 0 of the headline inputs."""
     import torch
     import torch.nn.functional as F
 
+    cores = _cpu_threads()
     q = tensors["q"][:1].float().cpu().transpose(1, 2).contiguous()
     k = tensors["k"][:1].float().cpu().transpose(1, 2).contiguous()
     v = tensors["v"][:1].float().cpu().transpose(1, 2).contiguous()
@@ -297,33 +330,104 @@ def cpu_baseline_train(tensors, hd):
 
     def once():
         qq, kk, vv = (t.clone().requires_grad_() for t in (q, k, v))
-        t0 = time.perf_counter()
         out = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=hd ** -0.5)
         out.backward(do)
-        return time.perf_counter() - t0
 
-    first = once()
-    reps = 3 if first < 8.0 else 1
-    times = [once() for _ in range(reps)]
-    t = statistics.median(times)
-    cpu_model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    t, reps = _median_time(once)
     return {
         "value": round(14 * unit / t / 1e12, 4),
         "unit": "TFLOPS",
-        "cores": torch.get_num_threads(),
+        "cores": cores,
         "kind": "port",
-        "sample": f"torch CPU scaled_dot_product_attention fp32 fwd+bwd, causal, batch 1 of the headline inputs "
+        "sample": f"torch CPU scaled_dot_product_attention fp32 fwd+bwd, causal, batch row 0 of the headline inputs "
                   f"(1x{seqlen}x{heads}x{hd}), median of {reps} after 1 warm-up, {t:.2f} s per step; "
-                  f"CPU: {cpu_model}",
+                  f"CPU: {_cpu_model()}",
     }
+
+
+def cpu_baseline_decode(device, n_seq=8):
+    """CPU decode of config c4's first n_seq sequences over L + 1 keys each: gather each
+    sequence's pages into a contiguous K/V (timed apart: the reference's
+    dense_prepare_cache, profile_kvcache_breakdown.py:182-195), then fp32 SDPA of
+    its one query over them (padded_sdpa_attention_only, :249-279).  GB/s of live
+    fp16 K/V bytes, the GPU leg's unit."""
+    import torch
+    import torch.nn.functional as F
+
+    cores = _cpu_threads()
+    b, h, hk, d, page = 64, 32, 8, 128, 256
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 32769, (b,), generator=g)
+    nblk = [(int(x) + 1 + page - 1) // page for x in lens]
+    perm = torch.randperm(sum(nblk), generator=g)
+    gd = torch.Generator(device=device).manual_seed(3)
+    total = sum(nblk)
+    k_cache = torch.randn((total, page, hk, d), generator=gd, device=device, dtype=torch.float16)
+    v_cache = torch.randn((total, page, hk, d), generator=gd, device=device, dtype=torch.float16)
+    q = torch.randn((b, 1, h, d), generator=g).to(torch.float16)
+    # The sampled sequences' pages, renumbered into a CPU page pool (copy not timed).
+    tables, pool_k, pool_v, off = [], [], [], 0
+    start = 0
+    for i in range(n_seq):
+        pages = perm[start : start + nblk[i]]
+        start += nblk[i]
+        pool_k.append(k_cache[pages.to(device)].cpu())
+        pool_v.append(v_cache[pages.to(device)].cpu())
+        tables.append(torch.arange(off, off + nblk[i]))
+        off += nblk[i]
+    del k_cache, v_cache
+    torch.cuda.empty_cache()
+    pk, pv = torch.cat(pool_k), torch.cat(pool_v)
+    ends = [int(lens[i]) + 1 for i in range(n_seq)]
+    scale = d ** -0.5
+
+    def gather():
+        return [(pk[tables[i]].reshape(-1, hk, d)[: ends[i]].contiguous(),
+                 pv[tables[i]].reshape(-1, hk, d)[: ends[i]].contiguous()) for i in range(n_seq)]
+
+    kv = gather()
+
+    def attend():
+        for i in range(n_seq):
+            kk = kv[i][0].float().transpose(0, 1).repeat_interleave(h // hk, dim=0)[None]
+            vv = kv[i][1].float().transpose(0, 1).repeat_interleave(h // hk, dim=0)[None]
+            F.scaled_dot_product_attention(q[i : i + 1].float().transpose(1, 2), kk, vv, scale=scale)
+
+    t_g, n_g = _median_time(gather, min_seconds=5.0)
+    t_a, n_a = _median_time(attend, min_seconds=5.0)
+    kv_bytes = sum(ends) * hk * d * 2 * 2
+    return {
+        "value": round(kv_bytes / (t_g + t_a) / 1e9, 2),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "gather_ms": round(t_g * 1e3, 2),
+        "attention_ms": round(t_a * 1e3, 2),
+        "sample": f"config c4's first {n_seq} sequences ({sum(ends)} keys, 32 q / 8 kv heads, d128): paged K/V gathered "
+                  f"to contiguous per sequence (median of {n_g}), then torch CPU scaled_dot_product_attention fp32 of "
+                  f"the one query (median of {n_a}); CPU: {_cpu_model()}",
+    }
+
+
+def sweep_legs(device, steps, warmup):
+    """benchmark.sh:17-38's shapes (batch 4, 16 heads): head_dim 64 / 128, causal or not,
+    seqlen 4096 and 8192; forward and backward TFLOPS per shape."""
+    import torch
+
+    out = {}
+    for hd in (64, 128):
+        for causal in (False, True):
+            for s in (4096, 8192):
+                launches, tensors = train_step_setup(4, s, 16, hd, 7, device, causal)
+                ms, per = Timed(launches).run(steps, warmup)
+                rep, _, _ = train_report(4, s, 16, hd, ms, per, causal)
+                out[f"hd{hd}_{'causal' if causal else 'full'}_s{s}"] = {
+                    "fwd_tflops": rep["fwd_tflops"], "bwd_tflops": rep["bwd_tflops"],
+                    "fwd_frac_fp16_peak": round(rep["fwd_tflops"] / PEAK_FP16_TFLOPS, 4),
+                    "bwd_frac_fp16_peak": round(rep["bwd_tflops"] / PEAK_FP16_TFLOPS, 4)}
+                del launches, tensors
+                torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -401,6 +505,11 @@ def main():
             torch.cuda.empty_cache()
 
     if args.only in ("all", "train") and not args.no_8k:
+        log("sweep: b4 h16, head_dim 64/128, causal and not, seqlen 4096/8192 (seed 7)")
+        result["sweep_b4_h16"] = sweep_legs(device, max(3, args.steps // 4), max(1, args.warmup // 4))
+        log(f"sweep: {result['sweep_b4_h16']}")
+
+    if args.only in ("all", "train") and not args.no_8k:
         log("varlen c3: 16 causal sequences, GQA 32/8, d128 (seed 2)")
         launches, info, unit, outs = varlen_setup(device)
         ms_v, perv = Timed(launches).run(max(3, args.steps // 2), max(1, args.warmup // 2))
@@ -436,6 +545,10 @@ def main():
         log(f"decode: {info}")
         del launches, outs
         torch.cuda.empty_cache()
+        if not args.skip_cpu:
+            log("cpu baseline for decode (c4 sample: gather, then torch CPU SDPA)")
+            result["cpu_baseline_decode"] = cpu_baseline_decode(device)
+            log(f"cpu decode: {result['cpu_baseline_decode']}")
         if not args.no_8k:
             # The same decode with a 4096-key sliding window (an upstream option the
             # reference rejects): the kernel skips the tiles outside the window.
