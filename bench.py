@@ -231,7 +231,9 @@ def varlen_setup(device, seed=2):
     scale = d ** -0.5
     fa = fa_capi.fwd_args(q, k, v, o, lse, scale, True, cu_d, cu_d, mx, mx)
     ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, scale, True, cu_d, cu_d, mx, mx)
-    # The dK/dV work items in longest-first order (built on the device by fa_bwd_dkdv).
+    # The work items in longest-first order (built on the device by fa_fwd, fa_bwd_dq and fa_bwd_dkdv).
+    forder = torch.empty(max(1, fa_capi.load().fa_fwd_order_len(ctypes.byref(fa))), dtype=torch.int32, device=device)
+    fa.work_order = forder.data_ptr()
     order = torch.empty(max(1, fa_capi.load().fa_bwd_order_len(ctypes.byref(ba))), dtype=torch.int32, device=device)
     ba.work_order = order.data_ptr()
     launches = [
@@ -241,7 +243,7 @@ def varlen_setup(device, seed=2):
     ]
     unit = h * d * sum(int(n) * (int(n) + 1) // 2 for n in lens)
     info = {"sequences": 16, "total_tokens": total, "max_seqlen": mx, "heads": h, "heads_k": hk, "head_dim": d}
-    return launches, info, unit, dict(o=o, dq=dq, dk=dk, dv=dv, order=order)
+    return launches, info, unit, dict(o=o, dq=dq, dk=dk, dv=dv, order=order, forder=forder)
 
 
 def longctx_setup(device, seed=4):

@@ -18,6 +18,7 @@
 // feeds dQ^T += K^T dS^T straight from the accumulators.
 // dK/dV kernel: 4 waves x 32 keys; S = Q K^T and dP = dO V^T put queries on
 // M so P and dS feed dV^T += dO^T P and dK^T += Q^T dS.
+#include <algorithm>
 #include <type_traits>
 
 #include "fa_common.h"
@@ -83,11 +84,23 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int col = lane & 31, hh = lane >> 5;
-    const int bh_count = a.batch * a.nheads;
-    const int bh = blockIdx.x % bh_count;
-    int mb = blockIdx.x / bh_count;
-    if (CAUSAL) mb = num_m_blocks - 1 - mb;
-    const int b = bh / a.nheads, h = bh - b * a.nheads;
+    int b, h, mb;
+    if (a.work_order && a.cu_seqlens_q) {
+        // Item of the device-built order (heads fastest); -1: no query rows.
+        const int nnb = (a.seqlen_k + 127) / 128;
+        const int it = a.work_order[int64_t(a.batch) * nnb + blockIdx.x / a.nheads];
+        if (it < 0) return;
+        b = __builtin_amdgcn_readfirstlane(it / num_m_blocks);
+        mb = __builtin_amdgcn_readfirstlane(it - b * num_m_blocks);
+        h = blockIdx.x % a.nheads;
+    } else {
+        const int bh_count = a.batch * a.nheads;
+        const int bh = blockIdx.x % bh_count;
+        mb = blockIdx.x / bh_count;
+        if (CAUSAL) mb = num_m_blocks - 1 - mb;
+        b = bh / a.nheads;
+        h = bh - b * a.nheads;
+    }
     const int hk = h / (a.nheads / a.nheads_k);
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
     const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
@@ -241,24 +254,15 @@ struct DkvCfg {
     static_assert(XCH <= LDS, "partial-sum exchange reuses the tiles' LDS");
 };
 
-// Varlen dK/dV work order.  Item it = b * nnb + nb is key block nb of
-// sequence b; its work is the number of query rows that see the block
-// (causal: min(sq, sk - 128 nb), else sq).  One workgroup counting-sorts the
-// items by that number in 64-row buckets, largest first (a histogram, a scan
-// over the buckets in descending order, then a scatter through per-bucket
-// cursors), and fills the rest of the list with -1 (no key in the block), so
-// the dK/dV grid starts the longest items first and its empty workgroups come
-// last.  Order within a bucket follows the LDS atomics; every item's result is
-// independent of it.
-constexpr int kOrderThreads = 1024, kOrderBuckets = 1024;
-static_assert(kOrderThreads == kOrderBuckets, "one histogram bucket and one scan slot per thread");
-
+// Varlen work orders (order_items in fa_common.h).  dK/dV: item it = b * nnb
+// + nb is key block nb of sequence b, its work the number of query rows that
+// see the block (causal: min(sq, sk - 128 nb), else sq), in 64-row buckets;
+// dQ: item it = b * nmb + mb is query block mb (128 rows), its work the keys
+// the block's last row sees (causal: min(sk, 128 (mb + 1) + sk - sq), else
+// sk), in 64-key buckets.  The list of the dK/dV items comes first in
+// work_order, that of the dQ items after it (fa_bwd_order_len).
 __global__ __launch_bounds__(kOrderThreads) void bwd_order_kernel(const fa_bwd_args a, const int nnb) {
-    __shared__ int hist[kOrderBuckets];
-    __shared__ int scan[kOrderBuckets];
-    const int tid = threadIdx.x;
-    const int n_items = a.batch * nnb;
-    auto bucket = [&](int it) {
+    order_items(a.batch * nnb, [&](int it) {
         const int b = it / nnb, nb = it - b * nnb;
         const int sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
         const int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.seqlen_q;
@@ -266,32 +270,19 @@ __global__ __launch_bounds__(kOrderThreads) void bwd_order_kernel(const fa_bwd_a
         if (k0 >= sk) return -1;
         const int rows = a.causal ? max(0, min(sq, sk - k0)) : max(sq, 0);
         return min(rows >> 6, kOrderBuckets - 1);
-    };
-    hist[tid] = 0;
-    __syncthreads();
-    for (int it = tid; it < n_items; it += kOrderThreads) {
-        const int k = bucket(it);
-        if (k >= 0) atomicAdd(&hist[k], 1);
-    }
-    __syncthreads();
-    // Inclusive scan of the counts in descending bucket order (slot t = bucket 1023 - t).
-    const int c = hist[kOrderBuckets - 1 - tid];
-    scan[tid] = c;
-    __syncthreads();
-    for (int d = 1; d < kOrderBuckets; d <<= 1) {
-        const int v = tid >= d ? scan[tid - d] : 0;
-        __syncthreads();
-        scan[tid] += v;
-        __syncthreads();
-    }
-    hist[kOrderBuckets - 1 - tid] = scan[tid] - c;  // first slot of the bucket
-    const int total = scan[kOrderBuckets - 1];
-    __syncthreads();
-    for (int it = tid; it < n_items; it += kOrderThreads) {
-        const int k = bucket(it);
-        if (k >= 0) a.work_order[atomicAdd(&hist[k], 1)] = it;
-    }
-    for (int i = total + tid; i < n_items; i += kOrderThreads) a.work_order[i] = -1;
+    }, a.work_order, false);
+}
+
+__global__ __launch_bounds__(kOrderThreads) void dq_order_kernel(const fa_bwd_args a, const int nnb, const int nmb) {
+    order_items(a.batch * nmb, [&](int it) {
+        const int b = it / nmb, mb = it - b * nmb;
+        const int sq = a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b];
+        const int sk = a.cu_seqlens_k ? a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b] : a.seqlen_k;
+        const int m0 = mb * 128;
+        if (m0 >= sq) return -1;
+        const int keys = a.causal ? max(0, min(sk, m0 + 128 + sk - sq)) : sk;
+        return min(keys >> 6, kOrderBuckets - 1);
+    }, a.work_order + int64_t(a.batch) * nnb, false);
 }
 
 template <int HD, bool CAUSAL>
@@ -607,6 +598,13 @@ static int launch_dq(const fa_bwd_args &a, hipStream_t s) {
     const int64_t grid = int64_t(nmb) * a.batch * a.nheads;
     if (grid == 0) return FA_OK;
     if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+    static_assert(DqCfg<HD>::BM == 128, "dq_order_kernel and fa_bwd_order_len assume 128-query blocks");
+    if (a.work_order && a.cu_seqlens_q) {
+        const int nnb = (a.seqlen_k + 127) / 128;
+        hipLaunchKernelGGL(dq_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, a, nnb, nmb);
+        const int rc = int(hipGetLastError());
+        if (rc) return rc;
+    }
     hipLaunchKernelGGL((bwd_dq_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a, nmb);
     return int(hipGetLastError());
 }
@@ -668,8 +666,10 @@ extern "C" int fa_bwd_dkdv(const fa_bwd_args *args, void *stream) {
 }
 
 extern "C" size_t fa_bwd_order_len(const fa_bwd_args *a) {
-    if (!a || a->batch <= 0 || a->seqlen_k <= 0) return 0;
-    return size_t(a->batch) * size_t((a->seqlen_k + 127) / 128);
+    if (!a || a->batch <= 0) return 0;
+    const size_t nnb = size_t((std::max(a->seqlen_k, 0) + 127) / 128);
+    const size_t nmb = size_t((std::max(a->lse_seqlen, 0) + 127) / 128);
+    return size_t(a->batch) * (nnb + nmb);
 }
 
 extern "C" int fa_bwd(const fa_bwd_args *args, void *stream) {

@@ -329,6 +329,56 @@ __device__ __forceinline__ f16x8 pack8(const f32x16 &acc, int base) {
     return r;
 }
 
+// ---------------------------------------------------------------------------
+// Longest-first work lists for varlen grids.  One workgroup of kOrderThreads
+// counting-sorts items [0, n_items) by bucket(it) (0 .. kOrderBuckets - 1,
+// larger = more work; -1 = no work): a histogram, a scan over the buckets in
+// descending order, then a scatter through per-bucket cursors.  out[] gets the
+// items largest bucket first, then the empty items (their ids when keep_empty,
+// for kernels that still have padding to write, else -1).  Order within a
+// bucket follows the LDS atomics; every item is computed independently, so
+// results do not depend on it.
+constexpr int kOrderThreads = 1024, kOrderBuckets = 1024;
+
+template <class Bucket>
+__device__ __forceinline__ void order_items(int n_items, Bucket bucket, int32_t *out, bool keep_empty) {
+    static_assert(kOrderThreads == kOrderBuckets, "one histogram bucket and one scan slot per thread");
+    __shared__ int hist[kOrderBuckets];
+    __shared__ int scan[kOrderBuckets];
+    __shared__ int n_empty;
+    const int tid = threadIdx.x;
+    hist[tid] = 0;
+    if (tid == 0) n_empty = 0;
+    __syncthreads();
+    for (int it = tid; it < n_items; it += kOrderThreads) {
+        const int k = bucket(it);
+        if (k >= 0) atomicAdd(&hist[k], 1);
+    }
+    __syncthreads();
+    // Inclusive scan of the counts in descending bucket order (slot t = bucket kOrderBuckets - 1 - t).
+    const int c = hist[kOrderBuckets - 1 - tid];
+    scan[tid] = c;
+    __syncthreads();
+    for (int d = 1; d < kOrderBuckets; d <<= 1) {
+        const int v = tid >= d ? scan[tid - d] : 0;
+        __syncthreads();
+        scan[tid] += v;
+        __syncthreads();
+    }
+    hist[kOrderBuckets - 1 - tid] = scan[tid] - c;  // first slot of the bucket
+    const int total = scan[kOrderBuckets - 1];
+    __syncthreads();
+    for (int it = tid; it < n_items; it += kOrderThreads) {
+        const int k = bucket(it);
+        if (k >= 0)
+            out[atomicAdd(&hist[k], 1)] = it;
+        else if (keep_empty)
+            out[total + atomicAdd(&n_empty, 1)] = it;
+    }
+    if (!keep_empty)
+        for (int i = total + tid; i < n_items; i += kOrderThreads) out[i] = -1;
+}
+
 // Per-batch extents of a dense or packed (varlen) batch.
 struct SeqInfo {
     int q_start, sq, k_start, sk;

@@ -80,12 +80,21 @@ struct FwdWork {
 // (its LSE padding is then written here).
 template <int BM, bool CAUSAL>
 __device__ __forceinline__ bool fwd_work(const fa_fwd_args &a, int num_m_blocks, FwdWork &w) {
-    const int bh_count = a.batch * a.nheads;
-    const int bh = blockIdx.x % bh_count;
-    int mb = blockIdx.x / bh_count;
-    if (CAUSAL) mb = num_m_blocks - 1 - mb;  // causal blocks are issued heaviest first
-    w.b = bh / a.nheads;
-    w.h = bh - w.b * a.nheads;
+    int mb;
+    if (a.work_order && a.cu_seqlens_q) {
+        // Item of the device-built order (heads fastest), longest first.
+        const int it = a.work_order[blockIdx.x / a.nheads];
+        w.b = __builtin_amdgcn_readfirstlane(it / num_m_blocks);
+        mb = __builtin_amdgcn_readfirstlane(it - w.b * num_m_blocks);
+        w.h = blockIdx.x % a.nheads;
+    } else {
+        const int bh_count = a.batch * a.nheads;
+        const int bh = blockIdx.x % bh_count;
+        mb = blockIdx.x / bh_count;
+        if (CAUSAL) mb = num_m_blocks - 1 - mb;  // causal blocks are issued heaviest first
+        w.b = bh / a.nheads;
+        w.h = bh - w.b * a.nheads;
+    }
     w.hk = w.h / (a.nheads / a.nheads_k);
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
     const SeqInfo si = seq_info(w.b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k,
@@ -492,6 +501,31 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, con
     store_row<HD>(a, w, qi, hh, o, row);
 }
 
+// Varlen work order (order_items in fa_common.h): item it = b * nmb + mb is
+// query block mb (BM rows) of sequence b, its work about rows x keys seen by
+// the block's last row, in buckets of BM x 64; blocks past a sequence's end
+// come last (they still write LSE padding).
+template <int BM>
+__global__ __launch_bounds__(kOrderThreads) void fwd_order_kernel(const fa_fwd_args a, const int nmb) {
+    order_items(a.batch * nmb, [&](int it) {
+        const int b = it / nmb, mb = it - b * nmb;
+        const int sq = a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b];
+        const int sk = a.cu_seqlens_k ? a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b] : a.seqlen_k;
+        const int m0 = mb * BM;
+        if (m0 >= sq) return -1;
+        const int64_t rows = min(BM, sq - m0);
+        const int64_t keys = a.causal ? max(0, min(sk, m0 + BM + sk - sq)) : max(sk, 0);
+        return int(min<int64_t>(rows * keys / (BM * 64), kOrderBuckets - 1));
+    }, a.work_order, true);
+}
+
+template <int BM>
+static int launch_order(const fa_fwd_args &a, int nmb, hipStream_t stream) {
+    if (!a.work_order || !a.cu_seqlens_q) return FA_OK;
+    hipLaunchKernelGGL(fwd_order_kernel<BM>, dim3(1), dim3(kOrderThreads), 0, stream, a, nmb);
+    return int(hipGetLastError());
+}
+
 template <int HD, bool CAUSAL>
 static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
     // The ping-pong kernel when its grid fills the chip at least twice over;
@@ -502,6 +536,8 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
         const int64_t pp_grid = pp_m_blocks * a.batch * a.nheads;
         if (pp_grid >= 2 * int64_t(device_cus())) {
             if (pp_grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+            const int rc = launch_order<FwdCfg<HD, 512>::BM>(a, int(pp_m_blocks), stream);
+            if (rc) return rc;
             hipLaunchKernelGGL((fwd_pp_kernel<HD, CAUSAL>), dim3(unsigned(pp_grid)), dim3(512), 0, stream, a,
                                int(pp_m_blocks));
             return int(hipGetLastError());
@@ -511,6 +547,8 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
     const int64_t grid = int64_t(num_m_blocks) * a.batch * a.nheads;
     if (grid == 0) return FA_OK;
     if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+    const int rc = launch_order<FwdCfg<HD, 256>::BM>(a, num_m_blocks, stream);
+    if (rc) return rc;
     hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(256), 0, stream, a, num_m_blocks);
     return int(hipGetLastError());
 }
@@ -533,4 +571,9 @@ extern "C" int fa_fwd(const fa_fwd_args *args, void *stream) {
     if (a.head_dim == 128)
         return a.causal ? fa::launch_fwd<128, true>(a, s) : fa::launch_fwd<128, false>(a, s);
     return a.causal ? fa::launch_fwd<64, true>(a, s) : fa::launch_fwd<64, false>(a, s);
+}
+
+extern "C" size_t fa_fwd_order_len(const fa_fwd_args *a) {
+    if (!a || a->batch <= 0 || a->lse_seqlen <= 0) return 0;
+    return size_t(a->batch) * size_t((a->lse_seqlen + 127) / 128);
 }

@@ -257,6 +257,9 @@ std::vector<at::Tensor> mha_varlen_fwd(at::Tensor q, at::Tensor k, at::Tensor v,
     a.lse_seqlen = max_seqlen_q;
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
+    // Query blocks ordered most work first on the device (sequences of mixed lengths).
+    at::Tensor work_order = at::empty({int64_t(std::max<size_t>(fa_fwd_order_len(&a), 1))}, cu_seqlens_q.options());
+    a.work_order = work_order.data_ptr<int32_t>();
     check_rc(fa_fwd(&a, current_stream()), "fa_fwd (varlen)");
     return {out, l};
 }
@@ -314,7 +317,7 @@ std::vector<at::Tensor> mha_varlen_bwd(at::Tensor q, at::Tensor k, at::Tensor v,
     a.lse_seqlen = max_seqlen_q;
     a.softmax_scale = softmax_scale;
     a.causal = is_causal ? 1 : 0;
-    // dK/dV work items ordered longest first on the device (sequences of mixed lengths).
+    // dQ and dK/dV work items ordered longest first on the device (sequences of mixed lengths).
     at::Tensor work_order = at::empty({int64_t(std::max<size_t>(fa_bwd_order_len(&a), 1))}, cu_seqlens_k.options());
     a.work_order = work_order.data_ptr<int32_t>();
     check_rc(fa_bwd(&a, current_stream()), "fa_bwd (varlen)");

@@ -41,7 +41,7 @@ class FaFwdArgs(ctypes.Structure):
         ("seqused_k_add", _i32),
         ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32), ("nheads", _i32), ("nheads_k", _i32),
         ("head_dim", _i32), ("lse_seqlen", _i32), ("softmax_scale", _f32), ("causal", _i32),
-        ("k_batch", _i32), ("status", _p),
+        ("k_batch", _i32), ("status", _p), ("work_order", _p),
     ]
 
 
@@ -104,6 +104,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fa_kv_num_splits.restype = ctypes.c_int
     lib.fa_kv_workspace_bytes.argtypes = [ctypes.POINTER(FaKvcacheArgs)]
     lib.fa_kv_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_fwd_order_len.argtypes = [ctypes.POINTER(FaFwdArgs)]
+    lib.fa_fwd_order_len.restype = ctypes.c_size_t
     lib.fa_bwd_order_len.argtypes = [ctypes.POINTER(FaBwdArgs)]
     lib.fa_bwd_order_len.restype = ctypes.c_size_t
     lib.fa_error_string.argtypes = [ctypes.c_int]
@@ -142,7 +144,7 @@ def call(name: str, args, stream=None) -> None:
 
 
 def fwd_args(q, k, v, o, lse, softmax_scale: float, causal: bool, cu_seqlens_q=None, cu_seqlens_k=None,
-             max_seqlen_q: int = 0, max_seqlen_k: int = 0) -> FaFwdArgs:
+             max_seqlen_q: int = 0, max_seqlen_k: int = 0, work_order=None) -> FaFwdArgs:
     packed = cu_seqlens_q is not None
     a = FaFwdArgs()
     a.q, a.k, a.v, a.o = (tensor_desc(x, packed) for x in (q, k, v, o))
@@ -159,6 +161,7 @@ def fwd_args(q, k, v, o, lse, softmax_scale: float, causal: bool, cu_seqlens_q=N
         a.lse_seqlen = q.shape[1]
     a.softmax_scale = softmax_scale
     a.causal = int(causal)
+    a.work_order = ptr(work_order)
     return a
 
 

@@ -69,8 +69,16 @@ typedef struct fa_fwd_args {
      * and, when status is set, ORs 1 (capacity) or 2 (cache row) into *status. */
     int32_t k_batch;                /* batches of k/v bounding k_batch_idx, 0 = unchecked */
     int32_t *status;                /* device int32 error word, or NULL          */
+    /* Optional workspace for varlen calls (cu_seqlens_q set), fa_fwd_order_len(args)
+     * int32s: fa_fwd then first lists the (sequence, query block) work items on
+     * the device, most work first, and launches the workgroups in that order;
+     * NULL keeps the natural order.  Results are the same either way. */
+    int32_t *work_order;
 } fa_fwd_args;
 
+/* Length in int32s of fa_fwd's work_order workspace: batch * ceil(lse_seqlen / 128).
+ * No counterpart in the reference (its grid is in natural order). */
+size_t fa_fwd_order_len(const fa_fwd_args *args);
 int fa_fwd(const fa_fwd_args *args, void *stream);
 
 /*
@@ -91,17 +99,20 @@ typedef struct fa_bwd_args {
     int32_t lse_seqlen;
     float softmax_scale;
     int32_t causal;
-    /* Optional workspace for varlen calls (cu_seqlens_k set), fa_bwd_order_len(args)
-     * int32s: fa_bwd_dkdv (and fa_bwd) then first list the (sequence, key block)
-     * work items on the device, most query rows first, and launch the dK/dV
-     * workgroups in that order; NULL keeps the natural order, which is longest
+    /* Optional workspace for varlen calls, fa_bwd_order_len(args) int32s:
+     * fa_bwd_dkdv (cu_seqlens_k set) first lists the (sequence, key block)
+     * work items on the device, most query rows first, and launches the dK/dV
+     * workgroups in that order, and fa_bwd_dq (cu_seqlens_q set) does the same
+     * for its (sequence, query block) items, most keys first, in the second
+     * part of the workspace; NULL keeps the natural order, which is longest
      * first only when every sequence has the same length.  Results are the same
      * either way (each item is computed independently). */
     int32_t *work_order;
 } fa_bwd_args;
 
-/* Length in int32s of the work_order workspace: batch * ceil(seqlen_k / 128).  No
- * counterpart in the reference (its dK/dV grid is in natural order). */
+/* Length in int32s of the work_order workspace: batch * (ceil(seqlen_k / 128) +
+ * ceil(lse_seqlen / 128)).  No counterpart in the reference (its grids are in
+ * natural order). */
 size_t fa_bwd_order_len(const fa_bwd_args *args);
 /* D = rowsum(dO * O) (flash_bwd_preprocess_kernel.h:23-96), stored negated in dsum plane 0. */
 int fa_bwd_preprocess(const fa_bwd_args *args, void *stream);
