@@ -55,8 +55,8 @@ def _run(cmd):
     return out
 
 
-def build_library(jobs: int) -> str:
-    objdir = os.path.join(HERE, "_build")
+def build_library(jobs: int, out_dir: str = HERE, obj_dir: str = None) -> str:
+    objdir = obj_dir or os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
     objs = []
 
@@ -67,19 +67,21 @@ def build_library(jobs: int) -> str:
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, KERNEL_SOURCES))
-    lib = os.path.join(HERE, LIB_NAME)
+    lib = os.path.join(out_dir, LIB_NAME)
     tmp = lib + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, f"-Wl,-rpath,{ROCM}/lib"])
     os.replace(tmp, lib)
     return lib
 
 
-def build_extension() -> str:
+def build_extension(out_dir: str = HERE) -> str:
+    """Link the extension against the libfa_mi355x.so already built in out_dir;
+    it finds that library at run time next to itself (rpath $ORIGIN)."""
     import torch
     from torch.utils import cpp_extension
 
     ext_suffix = sysconfig.get_config_var("EXT_SUFFIX")
-    out = os.path.join(HERE, "flash_attn_turing" + ext_suffix)
+    out = os.path.join(out_dir, "flash_attn_turing" + ext_suffix)
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     incs = cpp_extension.include_paths() + [sysconfig.get_paths()["include"], f"{ROCM}/include", INCLUDE]
     libdirs = cpp_extension.library_paths()
@@ -99,7 +101,7 @@ def build_extension() -> str:
         "-o",
         out + ".tmp",
         *[f"-L{p}" for p in libdirs],
-        f"-L{HERE}",
+        f"-L{out_dir}",
         "-lfa_mi355x",
         "-lc10",
         "-ltorch",
