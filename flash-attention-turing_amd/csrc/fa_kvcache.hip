@@ -507,20 +507,25 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
 }
 
 // ---------------------------------------------------------------------------
-// batch_order[r] = the sequence with the r-th largest key count (ties by index).
-constexpr int kOrderMaxBatch = 2048;
-// It also zeroes the work counter batch_order[batch] of the resident split kernel.
-__global__ __launch_bounds__(256) void kv_order_kernel(const fa_kvcache_args a) {
-    __shared__ int lens[kOrderMaxBatch];
+// batch_order[r] = the sequence with the r-th most keys, by a counting sort
+// over key-count buckets (exact below 32 keys, then 32 buckets per power of
+// two: about 3 % apart); order within a bucket is arbitrary, which changes no
+// result.  It also zeroes the work counter batch_order[batch] of the resident
+// split kernel.  One workgroup of kOrderThreads threads, O(batch) work.
+__device__ __forceinline__ int kv_len_bucket(int n) {
+    if (n < 32) return n;
+    const int msb = 31 - __clz(n);
+    return (msb - 4) * 32 + ((n >> (msb - 5)) & 31);
+}
+__global__ __launch_bounds__(kOrderThreads) void kv_order_kernel(const fa_kvcache_args a) {
     if (threadIdx.x == 0) a.batch_order[a.batch] = 0;
-    for (int i = threadIdx.x; i < a.batch; i += 256) lens[i] = a.cache_seqlens[i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < a.batch; i += 256) {
-        const int li = lens[i];
-        int rank = 0;
-        for (int j = 0; j < a.batch; ++j) rank += (lens[j] > li) || (lens[j] == li && j < i);
-        a.batch_order[rank] = i;
-    }
+    order_items(
+        a.batch,
+        [&](int b) {
+            const KvSeq sq = kv_seq(a, b);
+            return kv_len_bucket(sq.err ? 0 : sq.L0 + a.seqlen_new);
+        },
+        a.batch_order, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -685,10 +690,10 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     // With the batch_order workspace: rank the sequences and reset the work
     // counter, then run a resident grid of two workgroups per CU that deals
     // the items out in that order.  Without it: one workgroup per item.
-    const bool dyn = a.batch_order && a.batch <= fa::kOrderMaxBatch;
+    const bool dyn = a.batch_order != nullptr;
     unsigned grid = unsigned(gx);
     if (dyn) {
-        hipLaunchKernelGGL(fa::kv_order_kernel, dim3(1), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(fa::kv_order_kernel, dim3(1), dim3(fa::kOrderThreads), 0, s, a);
         const int rc = int(hipGetLastError());
         if (rc) return rc;
         grid = unsigned(std::min<int64_t>(gx, 2 * int64_t(fa::device_cus())));

@@ -9,6 +9,9 @@ calls the same entry points from C++.
 
 Tensors are passed as torch tensors only for convenience: ``tensor_desc``
 reads their data pointer and strides.  Nothing here allocates device memory.
+Each argument struct built here holds references to the tensors it points at
+(``_keep``), so their memory stays allocated for as long as the struct is
+used; a pointer assigned to a field afterwards is the caller's to keep alive.
 """
 
 import ctypes
@@ -162,6 +165,7 @@ def fwd_args(q, k, v, o, lse, softmax_scale: float, causal: bool, cu_seqlens_q=N
     a.softmax_scale = softmax_scale
     a.causal = int(causal)
     a.work_order = ptr(work_order)
+    a._keep = (q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, work_order)
     return a
 
 
@@ -186,6 +190,7 @@ def bwd_args(q, k, v, o, lse, dout, dq, dk, dv, dsum, softmax_scale: float, caus
     a.softmax_scale = softmax_scale
     a.causal = int(causal)
     a.work_order = ptr(work_order)
+    a._keep = (q, k, v, o, lse, dout, dq, dk, dv, dsum, cu_seqlens_q, cu_seqlens_k, work_order)
     return a
 
 
@@ -222,4 +227,6 @@ def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: floa
     a.rotary_dim = 0 if rotary_cos is None else 2 * rotary_cos.shape[1]
     a.rotary_seqlen = 0 if rotary_cos is None else rotary_cos.shape[0]
     a.rotary_interleaved = int(rotary_interleaved)
+    a._keep = (q, k_cache, v_cache, o, lse, cache_seqlens, k_new, v_new, cache_batch_idx, block_table, out_accum,
+               lse_accum, batch_order, status, cache_leftpad, alibi_slopes, rotary_cos, rotary_sin)
     return a

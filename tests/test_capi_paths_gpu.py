@@ -182,3 +182,53 @@ def test_paged_split_over_1024_pages(device, splits, order):
                                      num_splits=splits)
     torch.cuda.synchronize()
     assert torch.equal(o2.cpu(), out)
+
+
+def _len_bucket(n):
+    """The order kernel's key-count bucket: exact below 32, then 32 per power of two."""
+    if n < 32:
+        return n
+    msb = n.bit_length() - 1
+    return (msb - 4) * 32 + ((n >> (msb - 5)) & 31)
+
+
+@pytest.mark.gpu
+def test_order_kernel_large_batch(device):
+    """2500 sequences (more than one order-kernel round of 1024 threads): the
+    batch_order list is a permutation, sequences by non-increasing key-count
+    bucket, and the decode over that order matches the oracle (one invalid
+    sequence included: it sorts as empty and gets O = 0, LSE = 0)."""
+    g = torch.Generator().manual_seed(9400)
+    b, sq, h, hk, hd, cap, new, splits = 2500, 1, 4, 2, 64, 96, 1, 2
+    q, kc, vc, k, v, _ = _kv_inputs(g, b, sq, h, hk, hd, cap, new, False)
+    seqlens = torch.randint(0, cap - new + 1, (b,), generator=g, dtype=torch.int32)
+    seqlens[7] = cap  # cap + new > cap: invalid
+    qd, kcd, vcd = q.to(device), kc.clone().to(device), vc.clone().to(device)
+    o = torch.full_like(qd, 5.0)
+    lse = torch.full((b, h, sq), 5.0, dtype=torch.float32, device=device)
+    rows = b * h * sq
+    acc = torch.empty((splits * rows * (hd + 1),), dtype=torch.float32, device=device)
+    border = torch.full((b + 1,), -3, dtype=torch.int32, device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    a = fa_capi.kvcache_args(qd, kcd, vcd, o, lse, seqlens.to(device), hd ** -0.5, True, splits, k.to(device),
+                             v.to(device), out_accum=acc, lse_accum=acc[splits * rows * hd:], batch_order=border,
+                             status=status)
+    print(f"case order kernel b={b}", flush=True)
+    for name in ("fa_kv_append", "fa_kv_splitkv", "fa_kv_combine"):
+        fa_capi.call(name, a)
+    torch.cuda.synchronize()
+    order = border.cpu().tolist()
+    assert sorted(order[:b]) == list(range(b)), "batch_order must list every sequence once"
+    ends = [0 if i == 7 else int(n) + new for i, n in enumerate(seqlens.tolist())]
+    keys = [_len_bucket(ends[i]) for i in order[:b]]
+    assert all(x >= y for x, y in zip(keys, keys[1:])), "sequences must come most keys first"
+    assert order[b] > 0, "the work counter is reset, then counts the claimed items"
+    assert int(status.item()) == 1, "the invalid sequence is reported as a capacity error"
+    valid = [i for i in range(b) if i != 7]
+    sl = seqlens.clone()
+    sl[7] = 0
+    o_ref, l_ref, _, _ = kv_oracle(q[valid], kc[valid], vc[valid], k[valid], v[valid], sl[valid], None, None, True,
+                                   splits, None)
+    assert_2x("out", o.cpu()[valid], o_ref, o_ref.to(torch.float16))
+    assert_lse(lse.cpu()[valid], l_ref)
+    assert not o.cpu()[7].any() and not lse.cpu()[7].any()
