@@ -43,16 +43,17 @@ for _p in (PKG, REPO):
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 
-# HBM bytes per launch (read + write) of the headline-shape kernels, from
-# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --only train
-# --no-8k` / `--only decode`, scaled by the counters' reading of a 1 GiB copy
-# (FETCH x 2.0, WRITE x 1.0); summary in profiles/hbm_bytes_pmc_c2_c4.md.
-# Re-measured whenever a kernel changes; None where not measured.
+# HBM bytes per launch (read + write) of the headline-shape kernels (c2 for
+# fwd / dq / dkdv, c4 for kv_splitkv), from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE runs of `bench.py --only train` / `--only decode`, scaled by the
+# counters' reading of a 1 GiB copy (FETCH x 2.0, WRITE x 1.0); summary in
+# profiles/hbm_bytes_pmc.md.  Re-measured whenever a kernel changes; None
+# where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 7.989e8 + 6.816e7,
-    "bwd_dq": 6.386e8 + 7.353e7,
-    "bwd_dkdv": 7.886e8 + 1.500e8,
-    "kv_splitkv": 4.697e9 + 8.659e6,
+    "fwd": 4.522e8 + 6.881e7,
+    "bwd_dq": 6.359e8 + 7.349e7,
+    "bwd_dkdv": 7.494e8 + 1.413e8,
+    "kv_splitkv": 4.697e9 + 8.658e6,
 }
 
 
