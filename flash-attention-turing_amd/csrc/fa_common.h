@@ -195,19 +195,20 @@ __device__ __forceinline__ f16x4 lds_tr4(const char *base, int off) {
 
 // Placement of a natural [rows][KCH 16-byte chunks] fp16 tile in LDS: chunk c
 // of row r sits at chunk c ^ swz(r).  The XOR masks are chosen so that both
-// read patterns the kernels use are bank-conflict free (checked for 32 and
-// 64 four-byte banks, i.e. 8 or 16 lanes per ds_read_b128 phase and 16 or 32
-// lanes per ds_read_b64 phase):
+// read patterns the kernels use are bank-conflict free with 64 four-byte
+// banks (16 lanes per ds_read_b128 phase, 32 per ds_read_b64 phase):
 //   * MFMA A-operand rows: lanes read rows sigma(0..31) at one chunk pair;
 //   * lds_tr4 transposed reads: 8 rows x 64 bytes per instruction.
-// At head_dim 64 (8 chunks per row) a 16-lane b128 phase cannot be conflict
-// free; the 8-lane phases are.
+// At head_dim 64 two rows share a 256-byte bank window, so the 8 rows of
+// each parity in a 16-lane phase need 8 distinct chunks: the mask uses row
+// bits 1, 2 and 3 (an exhaustive search over XOR masks of the row bits for
+// both read patterns).  Both masks repeat every 16 rows, as TileCopier needs.
 template <int KCH>
 __device__ __forceinline__ int swz(int row) {
     if constexpr (KCH == 16)
         return ((row & 1) ? 4 : 0) ^ ((row & 2) ? 10 : 0) ^ ((row & 4) ? 2 : 0) ^ ((row & 8) ? 1 : 0);
     else
-        return ((row & 1) ? 2 : 0) ^ ((row & 2) ? 4 : 0) ^ ((row & 8) ? 1 : 0);
+        return ((row & 2) ? 4 : 0) ^ ((row & 4) ? 1 : 0) ^ ((row & 8) ? 2 : 0);
 }
 // Byte offset of (row, chunk) in such a tile.
 template <int HD>
