@@ -210,11 +210,6 @@ __device__ __forceinline__ int swz(int row) {
     else
         return ((row & 2) ? 4 : 0) ^ ((row & 4) ? 1 : 0) ^ ((row & 8) ? 2 : 0);
 }
-// Byte offset of (row, chunk) in such a tile.
-template <int HD>
-__device__ __forceinline__ int tile_off(int row, int chunk) {
-    return row * (HD * 2) + ((chunk ^ swz<HD / 8>(row)) << 4);
-}
 
 // Copy rows [row0, row0 + ROWS) of a [rows][HD] fp16 source (row stride rs,
 // rows clamped to <= last_row) into a swizzled natural tile with DMA: the NT
