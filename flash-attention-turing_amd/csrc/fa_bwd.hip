@@ -175,6 +175,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         if (nb + 1 < n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
         if (CAUSAL && MASK && n0 > q_lo + 31 + causal_off) return;  // no visible key for this wave
+        if (q_lo >= sq) return;                                      // no query row of the sequence
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
         f32x16 s[2], dp[2];

@@ -304,6 +304,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
         if (nb + 1 < w.n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
         if (CAUSAL && MASK && n0 > q_lo + 31 + w.causal_off) return;  // no visible key for this wave
+        if (q_lo >= w.sq) return;                                      // no query row of the sequence
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
         f32x16 s[2];
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, con
     // Last key this wave sees; blocks [0, nbw) hold its keys, and blocks
     // [0, n_full) need no mask for any of its queries.
     const int wave_last_key = CAUSAL ? min(w.sk - 1, q_lo + 31 + w.causal_off) : w.sk - 1;
-    const int nbw = max(0, min(w.n_blocks, (wave_last_key + BN) / BN));
+    const int nbw = q_lo < w.sq ? max(0, min(w.n_blocks, (wave_last_key + BN) / BN)) : 0;
     int n_full = min(w.n_blocks, w.sk / BN);
     if (CAUSAL) n_full = min(n_full, max(0, (q_lo + w.causal_off + 1) / BN));
 
