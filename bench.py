@@ -205,7 +205,69 @@ def decode_setup(device, seed=3, window=None):
              + sum(nblk) * 4 + b * 4)  # live block-table entries, seqlens
     info = {"batch": b, "heads": h, "heads_k": hk, "head_dim": d, "page_block_size": page, "num_splits": splits,
             "tokens": int(ends.sum()), "kv_bytes": kv_bytes, "bytes": kv_bytes + other}
-    return launches, info, dict(out=out, lse=lse)
+    return launches, info, dict(out=out, lse=lse, q=q, k_cache=k_cache, v_cache=v_cache, k_new=k_new, v_new=v_new,
+                                seqlens=seqlens, block_table=table_d)
+
+
+def time_calls(fn, steps, warmup):
+    """Median milliseconds of one fn() call between HIP events on the current
+    stream, with fn's host work (argument checks, allocation, host reads) in
+    the timeline."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    return statistics.median(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+
+
+def api_train_leg(device, steps, warmup):
+    """Config c2 through the drop-in API: flash_attn_func forward and its
+    autograd backward, output and gradients allocated by the call."""
+    import torch
+
+    import flash_attention_interface as fai
+
+    b, s, h, d = 4, 4096, 16, 128
+    g = torch.Generator().manual_seed(1)
+    q, k, v, do = (seeded_fp16((b, s, h, d), g, device) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def step():
+        out = fai.flash_attn_func(q, k, v, causal=True)
+        out.backward(do)
+        q.grad = k.grad = v.grad = None
+
+    ms = time_calls(step, steps, warmup)
+    unit = b * h * d * causal_pairs(s, s)
+    return {"ms_per_step": round(ms, 4), "step_tflops": round(14 * unit / (ms * 1e-3) / 1e12, 1)}
+
+
+def api_decode_leg(outs, info, steps, warmup):
+    """Config c4 through the drop-in API: flash_attn_with_kvcache with the
+    default host checks (validate=True: reads cache_seqlens on the host) and
+    without them (validate=False)."""
+    import flash_attention_interface as fai
+
+    res = {}
+    for validate in (True, False):
+        def call():
+            fai.flash_attn_with_kvcache(outs["q"], outs["k_cache"], outs["v_cache"], k=outs["k_new"],
+                                       v=outs["v_new"], cache_seqlens=outs["seqlens"],
+                                       block_table=outs["block_table"], causal=True, num_splits=8,
+                                       validate=validate)
+
+        ms = time_calls(call, steps, warmup)
+        res["validate" if validate else "no_validate"] = {"ms_per_call": round(ms, 4),
+                                                          "gbs": round(info["bytes"] / (ms * 1e-3) / 1e9, 1)}
+    return res
 
 
 def varlen_setup(device, seed=2):
@@ -496,6 +558,10 @@ def main():
             result["cpu_baseline"] = cpu_baseline_train(tensors, d)
         del launches, tensors
         torch.cuda.empty_cache()
+        log("c2 through the Python API (flash_attn_func + autograd backward)")
+        result["api_c2"] = api_train_leg(device, args.steps, args.warmup)
+        log(f"api c2: {result['api_c2']}")
+        torch.cuda.empty_cache()
 
         if not args.no_8k:
             log("north-star point: causal fwd+bwd b4 s8192 h16 d128 (seed 5)")
@@ -546,6 +612,9 @@ def main():
         info["frac_hbm_peak"] = round(info["gbs_call"] / PEAK_HBM_GBS, 4)
         result["decode_c4"] = info
         log(f"decode: {info}")
+        log("c4 through the Python API (flash_attn_with_kvcache)")
+        result["api_c4"] = api_decode_leg(outs, info, args.steps, args.warmup)
+        log(f"api c4: {result['api_c4']}")
         del launches, outs
         torch.cuda.empty_cache()
         if not args.skip_cpu:
