@@ -19,7 +19,11 @@ inputs already resident in HBM:
   ``--no-8k`` keeps only the headline shapes (c2, c4).
 
 Per-kernel durations come from HIP events recorded on the launch stream
-between the launches of the timed region.  The CPU baseline is PyTorch's CPU
+between the launches of the timed region.  A decode call is timed twice: as
+one fa_fwd_kvcache call (two launches: the append with the sequence ordering,
+then the split kernel, which with the split counts also combines), which gives
+``gbs_call``, and as its three entry points one by one, which gives the split
+kernel's own rate (``gbs_splitkv``).  The CPU baseline is PyTorch's CPU
 scaled_dot_product_attention (the reference test suite's oracle,
 test_flash_attn.py:313-368) in fp32 on a bounded sample of the same inputs.
 Prints ONE JSON line.
@@ -186,15 +190,13 @@ def decode_setup(device, seed=3, window=None):
     rows = b * h
     ws = torch.empty(splits * rows * (d + 1), dtype=torch.float32, device=device)
     order = torch.empty(b + 1, dtype=torch.int32, device=device)  # ranks + work counter
+    counts = torch.empty(b * hk, dtype=torch.int32, device=device)  # finished splits per (sequence, kv head)
     args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, seqlens, d ** -0.5, True, splits, k_new=k_new,
                                 v_new=v_new, block_table=table_d, out_accum=ws[: splits * rows * d],
                                 lse_accum=ws[splits * rows * d :], batch_order=order,
-                                window=window or (-1, -1))
-    launches = [
-        ("kv_append", lambda: fa_capi.call("fa_kv_append", args)),
-        ("kv_splitkv", lambda: fa_capi.call("fa_kv_splitkv", args)),
-        ("kv_combine", lambda: fa_capi.call("fa_kv_combine", args)),
-    ]
+                                window=window or (-1, -1), split_count=counts)
+    assert fa_capi.load().fa_kv_split_count_len(ctypes.byref(args)) == counts.numel()
+    launches, call = decode_launches(args)
     ends = lens + 1
     if window is not None and window[0] >= 0:
         ends = torch.clamp(ends, max=window[0] + 1)  # keys inside the window of the one query
@@ -205,8 +207,23 @@ def decode_setup(device, seed=3, window=None):
              + sum(nblk) * 4 + b * 4)  # live block-table entries, seqlens
     info = {"batch": b, "heads": h, "heads_k": hk, "head_dim": d, "page_block_size": page, "num_splits": splits,
             "tokens": int(ends.sum()), "kv_bytes": kv_bytes, "bytes": kv_bytes + other}
-    return launches, info, dict(out=out, lse=lse, q=q, k_cache=k_cache, v_cache=v_cache, k_new=k_new, v_new=v_new,
-                                seqlens=seqlens, block_table=table_d)
+    return launches, call, info, dict(out=out, lse=lse, q=q, k_cache=k_cache, v_cache=v_cache, k_new=k_new,
+                                      v_new=v_new, seqlens=seqlens, block_table=table_d)
+
+
+def decode_launches(args):
+    """The decode call two ways: the three entry points one by one (HIP events
+    between them time the split kernel, which with the split counts also
+    combines, so fa_kv_combine has nothing left to do), and fa_fwd_kvcache, the
+    whole call in two launches (append with ordering, split with combine)."""
+    import fa_capi
+
+    launches = [
+        ("kv_append", lambda: fa_capi.call("fa_kv_append", args)),
+        ("kv_splitkv", lambda: fa_capi.call("fa_kv_splitkv", args)),
+        ("kv_combine", lambda: fa_capi.call("fa_kv_combine", args)),
+    ]
+    return launches, [("kv_call", lambda: fa_capi.call("fa_fwd_kvcache", args))]
 
 
 def time_calls(fn, steps, warmup):
@@ -331,21 +348,19 @@ def longctx_setup(device, seed=4):
     nrow = b * h * sq
     ws = torch.empty(splits * nrow * (d + 1), dtype=torch.float32, device=device)
     order = torch.empty(b + 1, dtype=torch.int32, device=device)  # ranks + work counter
+    counts = torch.empty(b * h, dtype=torch.int32, device=device)  # finished splits per (sequence, kv head)
     args = fa_capi.kvcache_args(q, k_cache, v_cache, out, lse, lens.to(torch.int32).to(device), d ** -0.5, True,
                                 splits, k_new=k_new, v_new=v_new, cache_batch_idx=batch_idx.to(device),
                                 out_accum=ws[: splits * nrow * d], lse_accum=ws[splits * nrow * d :],
-                                batch_order=order)
-    launches = [
-        ("kv_append", lambda: fa_capi.call("fa_kv_append", args)),
-        ("kv_splitkv", lambda: fa_capi.call("fa_kv_splitkv", args)),
-        ("kv_combine", lambda: fa_capi.call("fa_kv_combine", args)),
-    ]
+                                batch_order=order, split_count=counts)
+    assert fa_capi.load().fa_kv_split_count_len(ctypes.byref(args)) == counts.numel()
+    launches, call = decode_launches(args)
     ends = lens + sq
     kv_bytes = int(ends.sum()) * h * d * 2 * 2
     other = 2 * b * sq * h * d * 2 + 2 * 2 * b * sq * h * d * 2 + nrow * 4 + 2 * b * 4
     info = {"cache_rows": rows, "capacity": cap, "batch": b, "seqlen_q": sq, "heads": h, "head_dim": d,
             "num_splits": splits, "tokens": int(ends.sum()), "kv_bytes": kv_bytes, "bytes": kv_bytes + other}
-    return launches, info, dict(out=out)
+    return launches, call, info, dict(out=out)
 
 
 def _cpu_threads():
@@ -599,14 +614,14 @@ def main():
 
     if args.only in ("all", "decode"):
         log("decode c4: paged split-KV with append (seed 3)")
-        launches, info, outs = decode_setup(device)
-        ms_dec, perd = Timed(launches).run(args.steps, args.warmup)
+        launches, call, info, outs = decode_setup(device)
+        _, perd = Timed(launches).run(args.steps, args.warmup)
+        _, perc = Timed(call).run(args.steps, args.warmup)
         assert torch.isfinite(outs["out"]).all(), "non-finite decode output"
-        t_all = sum(perd.values())
         info.update(
-            ms_per_call=round(ms_dec, 4),
+            ms_per_call=round(perc["kv_call"], 4),
             kernels_ms={k: round(v, 4) for k, v in perd.items()},
-            gbs_call=round(info["bytes"] / (t_all * 1e-3) / 1e9, 1),
+            gbs_call=round(info["bytes"] / (perc["kv_call"] * 1e-3) / 1e9, 1),
             gbs_splitkv=round(info["kv_bytes"] / (perd["kv_splitkv"] * 1e-3) / 1e9, 1),
         )
         info["frac_hbm_peak"] = round(info["gbs_call"] / PEAK_HBM_GBS, 4)
@@ -615,7 +630,7 @@ def main():
         log("c4 through the Python API (flash_attn_with_kvcache)")
         result["api_c4"] = api_decode_leg(outs, info, args.steps, args.warmup)
         log(f"api c4: {result['api_c4']}")
-        del launches, outs
+        del launches, call, outs
         torch.cuda.empty_cache()
         if not args.skip_cpu:
             log("cpu baseline for decode (c4 sample: gather, then torch CPU SDPA)")
@@ -625,31 +640,33 @@ def main():
             # The same decode with a 4096-key sliding window (an upstream option the
             # reference rejects): the kernel skips the tiles outside the window.
             log("decode c4 with window_size (4095, -1)")
-            launchesw, infow, outsw = decode_setup(device, window=(4095, -1))
-            msw, perw = Timed(launchesw).run(args.steps, args.warmup)
+            launchesw, callw, infow, outsw = decode_setup(device, window=(4095, -1))
+            _, perw = Timed(launchesw).run(args.steps, args.warmup)
+            _, percw = Timed(callw).run(args.steps, args.warmup)
             assert torch.isfinite(outsw["out"]).all(), "non-finite windowed decode output"
-            tw = sum(perw.values())
+            tw = percw["kv_call"]
             result["decode_c4_window4k"] = dict(
-                window=[4095, -1], kv_bytes_in_window=infow["kv_bytes"], ms_per_call=round(msw, 4),
+                window=[4095, -1], kv_bytes_in_window=infow["kv_bytes"], ms_per_call=round(tw, 4),
                 kernels_ms={k: round(v, 4) for k, v in perw.items()},
                 gbs_call=round(infow["bytes"] / (tw * 1e-3) / 1e9, 1),
-                speedup_vs_full_cache=round(info["ms_per_call"] / msw, 2))
+                speedup_vs_full_cache=round(info["ms_per_call"] / tw, 2))
             log(f"decode window: {result['decode_c4_window4k']}")
-            del launchesw, outsw
+            del launchesw, callw, outsw
             torch.cuda.empty_cache()
         if not args.no_8k:
             log("long-context c5: contiguous 8 x 131072 cache, remapped rows, 4-token append, 16 splits (seed 4)")
-            launches5, info5, outs5 = longctx_setup(device)
-            ms5, per5 = Timed(launches5).run(args.steps, args.warmup)
+            launches5, call5, info5, outs5 = longctx_setup(device)
+            _, per5 = Timed(launches5).run(args.steps, args.warmup)
+            _, perc5 = Timed(call5).run(args.steps, args.warmup)
             assert torch.isfinite(outs5["out"]).all(), "non-finite long-context output"
-            t5 = sum(per5.values())
-            info5.update(ms_per_call=round(ms5, 4), kernels_ms={k: round(v, 4) for k, v in per5.items()},
+            t5 = perc5["kv_call"]
+            info5.update(ms_per_call=round(t5, 4), kernels_ms={k: round(v, 4) for k, v in per5.items()},
                          gbs_call=round(info5["bytes"] / (t5 * 1e-3) / 1e9, 1),
                          gbs_splitkv=round(info5["kv_bytes"] / (per5["kv_splitkv"] * 1e-3) / 1e9, 1))
             info5["frac_hbm_peak"] = round(info5["gbs_call"] / PEAK_HBM_GBS, 4)
             result["longctx_c5"] = info5
             log(f"long-context: {info5}")
-            del launches5, outs5
+            del launches5, call5, outs5
             torch.cuda.empty_cache()
         if args.only == "decode":
             result.update(metric="paged split-KV decode HBM GB/s", value=info["gbs_call"], unit="GB/s",

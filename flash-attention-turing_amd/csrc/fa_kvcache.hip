@@ -26,11 +26,13 @@
 // states through LDS at the end.  Paged, remapped and contiguous caches take
 // the same tile order and the same arithmetic, so their results are
 // bit-identical for the same logical cache.  Work items are ordered with the
-// sequence rank slowest: when the caller passes a batch_order workspace, a
-// one-workgroup kernel first ranks the sequences by key count (longest first)
-// and a resident grid of two workgroups per CU deals the items out from a
-// device counter in that order, so the longest sequences start first, the
-// short ones fill the end, and no workgroup is relaunched between items.
+// sequence rank slowest: when the caller passes a batch_order workspace, one
+// workgroup of the append launch first ranks the sequences by key count
+// (longest first) and a resident grid of two workgroups per CU deals the items
+// out from a device counter in that order, so the longest sequences start
+// first, the short ones fill the end, and no workgroup is relaunched between
+// items.  With split counts as well, the last split item of each row tile to
+// finish combines the tile's partials, so a decode call is two launches.
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -125,13 +127,13 @@ __device__ __forceinline__ u32x4 rotary8(const fa_kvcache_args &a, const u32x4 x
 }
 
 // ---------------------------------------------------------------------------
-// Append: one thread per 16-byte chunk of k_new / v_new (with rotary_dim > 0,
-// the key chunks below rotary_dim are rotated at their position first).
+// Append of 16-byte chunk idx of k_new / v_new, one per thread (with
+// rotary_dim > 0, the key chunks below rotary_dim are rotated at their
+// position first).
 template <int HD>
-__global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a) {
+__device__ __forceinline__ void append_chunk(const fa_kvcache_args &a, const int64_t idx) {
     constexpr int KCH = HD / 8;
     const int64_t total = int64_t(a.batch) * a.seqlen_new * a.nheads_k * KCH;
-    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= total) return;
     const int c = int(idx % KCH);
     int64_t rest = idx / KCH;
@@ -156,6 +158,146 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const fa_kvcache_args a)
     if (8 * c < a.rotary_dim) kx = rotary8(a, kx, ks - 8 * c, 8 * c, pos);
     *reinterpret_cast<u32x4 *>(kd) = kx;
     *reinterpret_cast<u32x4 *>(vd) = ldg16(vs);
+}
+
+// ---------------------------------------------------------------------------
+// Append and ordering in one launch of kOrderThreads-thread workgroups.  The
+// first order_wgs workgroups (0 or 1) rank the sequences: batch_order[r] = the
+// sequence with the r-th most keys, by a counting sort over key-count buckets
+// (exact below 32 keys, then 32 buckets per power of two: about 3 % apart;
+// order within a bucket is arbitrary, which changes no result), and zero the
+// split kernel's work counter batch_order[batch] and its n_count split counts.
+// The other workgroups append one 16-byte chunk per thread.  The two parts
+// touch disjoint memory (the ranking reads cache_seqlens only).
+__device__ __forceinline__ int kv_len_bucket(int n) {
+    if (n < 32) return n;
+    const int msb = 31 - __clz(n);
+    return (msb - 4) * 32 + ((n >> (msb - 5)) & 31);
+}
+template <int HD>
+__global__ __launch_bounds__(kOrderThreads) void kv_prep_kernel(const fa_kvcache_args a, const int order_wgs,
+                                                                int32_t *const count, const int n_count) {
+    if (int(blockIdx.x) < order_wgs) {
+        if (threadIdx.x == 0) a.batch_order[a.batch] = 0;
+        for (int i = threadIdx.x; i < n_count; i += kOrderThreads) count[i] = 0;
+        order_items(
+            a.batch,
+            [&](int b) {
+                const KvSeq sq = kv_seq(a, b);
+                return kv_len_bucket(sq.err ? 0 : sq.L0 + a.seqlen_new);
+            },
+            a.batch_order, true);
+        return;
+    }
+    append_chunk<HD>(a, int64_t(blockIdx.x - order_wgs) * kOrderThreads + threadIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Combine of one output row r (of batch * nheads * seqlen_q) by one wave.  Lane
+// s reads split s's LSE (further rounds past 64 splits) while the partial
+// outputs of the first kPreSplits splits are loaded at the same time; the
+// maximum and the weight sum are wave reductions, and each lane sums HD / 64
+// output elements over the splits with the weight exp(lse_s - lse_total)
+// taken from lane s.  Run by the combine kernel, or inside the split kernel by
+// the last split item of a row tile.
+constexpr int kPreSplits = 16;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// Split partials as the combine reads them.  Inside the split kernel
+// (COHERENT) they are device-scope atomic loads, which see what device-scope
+// stores of other workgroups left whatever this XCD's L2 holds (the partials
+// are stored that way); the combine kernel, launched after the split kernel,
+// reads them plainly.
+template <bool COHERENT>
+__device__ __forceinline__ float load_part(const float *p) {
+    if constexpr (COHERENT)
+        return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        return *p;
+}
+template <bool COHERENT, int DPL>
+__device__ __forceinline__ float __attribute__((ext_vector_type(DPL))) load_part_vec(const float *p) {
+    typedef float fdpl __attribute__((ext_vector_type(DPL)));
+    if constexpr (!COHERENT) {
+        return *reinterpret_cast<const fdpl *>(p);
+    } else if constexpr (DPL == 1) {
+        fdpl v;
+        v[0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return v;
+    } else {
+        static_assert(DPL == 2, "one 64-bit load per lane");
+        const uint64_t u =
+            __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return __builtin_bit_cast(fdpl, u);
+    }
+}
+
+template <int HD, bool COHERENT>
+__device__ __forceinline__ void combine_row(const fa_kvcache_args &a, const int r, int lane) {
+    // Opaque to the optimiser: keeps the addresses below from being hoisted out
+    // of the split kernel's item loop into registers live through its tile loop.
+    asm volatile("" : "+v"(lane));
+    constexpr int DPL = HD / 64;  // output elements per lane
+    typedef float fdpl __attribute__((ext_vector_type(DPL)));
+    const int nrow = a.batch * a.nheads * a.seqlen_q;
+    const int S = a.num_splits;
+    auto part = [&](int s) {
+        return load_part_vec<COHERENT, DPL>(a.out_accum + (int64_t(s) * nrow + r) * HD + DPL * lane);
+    };
+    auto lse_of = [&](int s) { return load_part<COHERENT>(a.lse_accum + int64_t(s) * nrow + r); };
+    // Splits past S re-read split S - 1 (finite) and get weight 0 below.
+    fdpl pre[kPreSplits];
+#pragma unroll
+    for (int s = 0; s < kPreSplits; ++s) pre[s] = part(min(s, S - 1));
+    const float lse0 = lane < S ? lse_of(lane) : -INFINITY;
+    float lmax = lse0;
+    for (int s0 = 64; s0 < S; s0 += 64)
+        if (s0 + lane < S) lmax = fmaxf(lmax, lse_of(s0 + lane));
+    lmax = wave_max(lmax);
+    float psum = 0.f;
+    if (lmax != -INFINITY) {
+        if (lane < S) psum = expf(lse0 - lmax);
+        for (int s0 = 64; s0 < S; s0 += 64)
+            if (s0 + lane < S) psum += expf(lse_of(s0 + lane) - lmax);
+    }
+    const float wsum = wave_sum(psum);
+    const bool live = lmax != -INFINITY && wsum > 0.f;
+    const float ltot = live ? lmax + logf(wsum) : -INFINITY;
+    fdpl acc;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+    if (live) {
+        const float w0 = lane < S ? expf(lse0 - ltot) : 0.f;
+        auto weight = [](float w, int s) {
+            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+        };
+#pragma unroll
+        for (int s = 0; s < kPreSplits; ++s) acc += weight(w0, s) * pre[s];  // lane s >= S holds w0 = 0
+        for (int s0 = 0; s0 < S; s0 += 64) {
+            const float w = s0 == 0 ? w0 : (s0 + lane < S ? expf(lse_of(s0 + lane) - ltot) : 0.f);
+            const int n = min(64, S - s0);
+#pragma unroll 1
+            for (int s = s0 == 0 ? kPreSplits : 0; s < n; ++s) acc += weight(w, s) * part(s0 + s);
+        }
+    }
+    const int qp = r % a.seqlen_q;
+    const int bh = r / a.seqlen_q;
+    const int h = bh % a.nheads, b = bh / a.nheads;
+    f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
+              int64_t(h) * a.o.head_stride + DPL * lane;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) op[i] = (f16)acc[i];
+    if (lane == 0) a.lse[r] = live ? ltot : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -195,17 +337,20 @@ __device__ __forceinline__ float tanh_fast(float x) {
 // CU) and each workgroup, after its first item blockIdx.x, takes the next
 // unclaimed item from a device counter, so no workgroup is relaunched and
 // the items are dealt out greedily in that order.  The counter
-// (batch_order[batch]) is zeroed by kv_order_kernel on the same stream.
+// (batch_order[batch]) is zeroed by kv_prep_kernel on the same stream.
+// With count (num_splits > 1, DYN) the split kernel also combines: count[(b *
+// nheads_k + hk) * row_tiles + rt] (zeroed by kv_prep_kernel) counts the
+// finished splits of that row tile, and the item that finishes last combines
+// the tile's rows with combine_row, as the combine kernel would.
 // EXT switches on the local window, softcap, ALiBi, cache_leftpad and rotary options
 // (a separate instance, so the plain kernel carries none of their work).
 template <int HD, bool DYN, bool EXT>
-__global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a,
-                                                                                   const int row_tiles,
-                                                                                   const int n_items) {
+__global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a, const int row_tiles,
+                                                            const int n_items, int32_t *const count) {
     using C = KvCfg<HD>;
     __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
     __shared__ int pages[C::MAX_PAGES];
-    __shared__ int next_item;
+    __shared__ int next_item, last_item;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
@@ -494,8 +639,32 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
                 op[d] = (f16)outv;
                 if (d == 0) a.lse[orow] = live ? lse : 0.f;
             } else {
-                a.out_accum[(int64_t(split) * nrow_all + orow) * HD + d] = outv;
-                if (d == 0) a.lse_accum[int64_t(split) * nrow_all + orow] = lse;
+                // Device-scope stores: the last split item of the tile may combine
+                // them on another XCD in this same launch.
+                __hip_atomic_store(a.out_accum + (int64_t(split) * nrow_all + orow) * HD + d, outv, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0)
+                    __hip_atomic_store(a.lse_accum + int64_t(split) * nrow_all + orow, lse, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (DYN && S > 1 && count) {
+            // The item counts itself done once every wave's partial stores have
+            // completed (vmcnt 0: written at device scope); the item that brings
+            // the count to S has seen all S items' stores complete and reads the
+            // partials with device-scope loads.  No cache-wide write-back or
+            // invalidate is needed (both would stall this XCD's L2 once per item).
+            wait_vmem();
+            __syncthreads();
+            if (tid == 0)
+                last_item = __hip_atomic_fetch_add(count + (int64_t(b) * a.nheads_k + hk) * row_tiles + rt, 1,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+            __syncthreads();
+            if (last_item) {
+                for (int c = wave; c < rows_here; c += kKvWaves) {
+                    const int r = rt * 32 + c;
+                    combine_row<HD, true>(a, (b * a.nheads + hk * G + r % G) * a.seqlen_q + r / G, lane);
+                }
             }
         }
         if constexpr (!DYN) break;
@@ -507,102 +676,12 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
 }
 
 // ---------------------------------------------------------------------------
-// batch_order[r] = the sequence with the r-th most keys, by a counting sort
-// over key-count buckets (exact below 32 keys, then 32 buckets per power of
-// two: about 3 % apart); order within a bucket is arbitrary, which changes no
-// result.  It also zeroes the work counter batch_order[batch] of the resident
-// split kernel.  One workgroup of kOrderThreads threads, O(batch) work.
-__device__ __forceinline__ int kv_len_bucket(int n) {
-    if (n < 32) return n;
-    const int msb = 31 - __clz(n);
-    return (msb - 4) * 32 + ((n >> (msb - 5)) & 31);
-}
-__global__ __launch_bounds__(kOrderThreads) void kv_order_kernel(const fa_kvcache_args a) {
-    if (threadIdx.x == 0) a.batch_order[a.batch] = 0;
-    order_items(
-        a.batch,
-        [&](int b) {
-            const KvSeq sq = kv_seq(a, b);
-            return kv_len_bucket(sq.err ? 0 : sq.L0 + a.seqlen_new);
-        },
-        a.batch_order, true);
-}
-
-// ---------------------------------------------------------------------------
-// Combine: one wave per (batch, head, qpos) row.  Lane s reads split s's LSE
-// (further rounds past 64 splits) while the partial outputs of the first
-// kPreSplits splits are loaded at the same time; the maximum and the weight
-// sum are wave reductions, and each lane sums HD / 64 output elements over
-// the splits with the weight exp(lse_s - lse_total) taken from lane s.
-constexpr int kPreSplits = 16;
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
-}
-
+// Combine kernel: one wave per (batch, head, qpos) row.
 template <int HD>
 __global__ __launch_bounds__(256) void kv_combine_kernel(const fa_kvcache_args a) {
-    constexpr int DPL = HD / 64;  // output elements per lane
-    typedef float fdpl __attribute__((ext_vector_type(DPL)));
-    const int nrow = a.batch * a.nheads * a.seqlen_q;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (r >= nrow) return;
-    const int S = a.num_splits;
-    auto part_ptr = [&](int s) {
-        return reinterpret_cast<const fdpl *>(a.out_accum + (int64_t(s) * nrow + r) * HD + DPL * lane);
-    };
-    // Splits past S re-read split S - 1 (finite) and get weight 0 below.
-    fdpl pre[kPreSplits];
-#pragma unroll
-    for (int s = 0; s < kPreSplits; ++s) pre[s] = *part_ptr(min(s, S - 1));
-    const float lse0 = lane < S ? a.lse_accum[int64_t(lane) * nrow + r] : -INFINITY;
-    float lmax = lse0;
-    for (int s0 = 64; s0 < S; s0 += 64)
-        if (s0 + lane < S) lmax = fmaxf(lmax, a.lse_accum[int64_t(s0 + lane) * nrow + r]);
-    lmax = wave_max(lmax);
-    float part = 0.f;
-    if (lmax != -INFINITY) {
-        if (lane < S) part = expf(lse0 - lmax);
-        for (int s0 = 64; s0 < S; s0 += 64)
-            if (s0 + lane < S) part += expf(a.lse_accum[int64_t(s0 + lane) * nrow + r] - lmax);
-    }
-    const float wsum = wave_sum(part);
-    const bool live = lmax != -INFINITY && wsum > 0.f;
-    const float ltot = live ? lmax + logf(wsum) : -INFINITY;
-    fdpl acc;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
-    if (live) {
-        const float w0 = lane < S ? expf(lse0 - ltot) : 0.f;
-        auto weight = [](float w, int s) {
-            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
-        };
-#pragma unroll
-        for (int s = 0; s < kPreSplits; ++s) acc += weight(w0, s) * pre[s];  // lane s >= S holds w0 = 0
-        for (int s0 = 0; s0 < S; s0 += 64) {
-            const float w = s0 == 0 ? w0
-                                    : (s0 + lane < S ? expf(a.lse_accum[int64_t(s0 + lane) * nrow + r] - ltot) : 0.f);
-            const int n = min(64, S - s0);
-#pragma unroll 1
-            for (int s = s0 == 0 ? kPreSplits : 0; s < n; ++s) acc += weight(w, s) * *part_ptr(s0 + s);
-        }
-    }
-    const int qp = r % a.seqlen_q;
-    const int bh = r / a.seqlen_q;
-    const int h = bh % a.nheads, b = bh / a.nheads;
-    f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
-              int64_t(h) * a.o.head_stride + DPL * lane;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) op[i] = (f16)acc[i];
-    if (lane == 0) a.lse[r] = live ? ltot : 0.f;
+    if (r >= a.batch * a.nheads * a.seqlen_q) return;
+    combine_row<HD, false>(a, r, threadIdx.x & 63);
 }
 
 static int check_kv(const fa_kvcache_args *p) {
@@ -653,59 +732,80 @@ extern "C" size_t fa_kv_workspace_bytes(const fa_kvcache_args *a) {
     return size_t(a->num_splits) * rows * (size_t(a->head_dim) + 1) * sizeof(float);
 }
 
-extern "C" int fa_kv_append(const fa_kvcache_args *args, void *stream) {
-    int rc = fa::check_kv(args);
-    if (rc) return rc;
-    const fa_kvcache_args &a = *args;
-    if (!a.k_new.ptr || a.seqlen_new == 0 || a.batch == 0) return FA_OK;
+extern "C" size_t fa_kv_split_count_len(const fa_kvcache_args *a) {
+    if (!a || a->num_splits <= 1 || a->batch <= 0 || a->nheads_k <= 0 || a->nheads <= 0 || a->seqlen_q <= 0)
+        return 0;
+    const int64_t rows = int64_t(a->nheads / a->nheads_k) * a->seqlen_q;
+    return size_t(int64_t(a->batch) * a->nheads_k * ((rows + 31) / 32));
+}
+
+namespace fa {
+namespace {
+
+bool has_append(const fa_kvcache_args &a) { return a.k_new.ptr && a.seqlen_new > 0 && a.batch > 0; }
+
+int check_append(const fa_kvcache_args &a) {
+    if (!has_append(a)) return FA_OK;
     if (!a.v_new.ptr || fa_check_tensor(a.k_new, true) || fa_check_tensor(a.v_new, true) ||
         fa_check_tensor(a.k_cache, true) || fa_check_tensor(a.v_cache, true))
         return FA_ERR_INVALID_ARG;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t total = int64_t(a.batch) * a.seqlen_new * a.nheads_k * (a.head_dim / 8);
-    const int64_t blocks = (total + 255) / 256;
-    if (a.head_dim == 128)
-        hipLaunchKernelGGL(fa::kv_append_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(fa::kv_append_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
-    return int(hipGetLastError());
+    return FA_OK;
 }
 
-extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
-    int rc = fa::check_kv(args);
-    if (rc) return rc;
-    const fa_kvcache_args &a = *args;
+// Work items of the split kernel: (batch, kv head, split, 32-row tile).
+int64_t split_items(const fa_kvcache_args &a) {
+    const int R = (a.nheads / a.nheads_k) * a.seqlen_q;
+    return int64_t(a.batch) * a.nheads_k * ((R + 31) / 32) * a.num_splits;
+}
+
+int check_split(const fa_kvcache_args &a) {
     if (fa_check_tensor(a.q, true) || fa_check_tensor(a.o, true) || fa_check_tensor(a.k_cache, true) ||
         fa_check_tensor(a.v_cache, true))
         return FA_ERR_INVALID_ARG;
     if (a.num_splits > 1 && (!a.out_accum || !a.lse_accum)) return FA_ERR_WORKSPACE;
-    const int R = (a.nheads / a.nheads_k) * a.seqlen_q;
-    const int row_tiles = (R + 31) / 32;
-    const int64_t gx = int64_t(a.batch) * a.nheads_k * row_tiles * a.num_splits;
+    if (split_items(a) > 0x7fffffff) return FA_ERR_INVALID_ARG;
+    return FA_OK;
+}
+
+// The split kernel combines its partials itself: a resident grid (batch_order)
+// with split counts and more than one split.
+bool fused_combine(const fa_kvcache_args &a) { return a.batch_order && a.split_count && a.num_splits > 1; }
+
+// kv_prep_kernel over the append's chunks (append) after one ordering workgroup (order).
+int launch_prep(const fa_kvcache_args &a, bool append, bool order, hipStream_t s) {
+    const int64_t chunks = append ? int64_t(a.batch) * a.seqlen_new * a.nheads_k * (a.head_dim / 8) : 0;
+    const int order_wgs = order ? 1 : 0;
+    const int64_t blocks = order_wgs + (chunks + kOrderThreads - 1) / kOrderThreads;
+    if (blocks == 0) return FA_OK;
+    if (blocks > 0x7fffffff) return FA_ERR_INVALID_ARG;
+    int32_t *count = order && fused_combine(a) ? a.split_count : nullptr;
+    const int n_count = count ? int(fa_kv_split_count_len(&a)) : 0;
+    if (a.head_dim == 128)
+        hipLaunchKernelGGL(kv_prep_kernel<128>, dim3(unsigned(blocks)), dim3(kOrderThreads), 0, s, a, order_wgs, count,
+                           n_count);
+    else
+        hipLaunchKernelGGL(kv_prep_kernel<64>, dim3(unsigned(blocks)), dim3(kOrderThreads), 0, s, a, order_wgs, count,
+                           n_count);
+    return int(hipGetLastError());
+}
+
+// The split kernel.  With batch_order (ranked and its counter reset by
+// launch_prep on the same stream): a resident grid of two workgroups per CU
+// that deals the items out in that order.  Without it: one workgroup per item.
+int launch_split(const fa_kvcache_args &a, hipStream_t s) {
+    const int64_t gx = split_items(a);
     if (gx == 0) return FA_OK;
-    if (gx > 0x7fffffff) return FA_ERR_INVALID_ARG;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    fa_kvcache_args run = a;
+    const int row_tiles = ((a.nheads / a.nheads_k) * a.seqlen_q + 31) / 32;
     const int n_items = int(gx);
-    // With the batch_order workspace: rank the sequences and reset the work
-    // counter, then run a resident grid of two workgroups per CU that deals
-    // the items out in that order.  Without it: one workgroup per item.
     const bool dyn = a.batch_order != nullptr;
-    unsigned grid = unsigned(gx);
-    if (dyn) {
-        hipLaunchKernelGGL(fa::kv_order_kernel, dim3(1), dim3(fa::kOrderThreads), 0, s, a);
-        const int rc = int(hipGetLastError());
-        if (rc) return rc;
-        grid = unsigned(std::min<int64_t>(gx, 2 * int64_t(fa::device_cus())));
-    } else {
-        run.batch_order = nullptr;  // natural order
-    }
+    const unsigned grid = unsigned(dyn ? std::min<int64_t>(gx, 2 * int64_t(device_cus())) : gx);
+    int32_t *count = fused_combine(a) ? a.split_count : nullptr;
     const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
     auto go = [&](auto hd_tag, auto dyn_tag, auto ext_tag) {
         constexpr int HD = decltype(hd_tag)::value;
         constexpr bool DYN = decltype(dyn_tag)::value, EXT = decltype(ext_tag)::value;
-        hipLaunchKernelGGL((fa::kv_splitkv_kernel<HD, DYN, EXT>), dim3(grid), dim3(fa::kKvThreads), 0, s, run,
-                           row_tiles, n_items);
+        hipLaunchKernelGGL((kv_splitkv_kernel<HD, DYN, EXT>), dim3(grid), dim3(kKvThreads), 0, s, a, row_tiles,
+                           n_items, count);
     };
     using H128 = std::integral_constant<int, 128>;
     using H64 = std::integral_constant<int, 64>;
@@ -721,42 +821,72 @@ extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
     return int(hipGetLastError());
 }
 
+// The combine kernel, unless there is one split or the split kernel combined.
+int launch_combine(const fa_kvcache_args &a, hipStream_t s) {
+    if (a.num_splits <= 1 || fused_combine(a)) return FA_OK;
+    const int64_t nrow = int64_t(a.batch) * a.nheads * a.seqlen_q;
+    if (nrow == 0) return FA_OK;
+    const int64_t blocks = (nrow + 3) / 4;
+    if (a.head_dim == 128)
+        hipLaunchKernelGGL(kv_combine_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(kv_combine_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
+    return int(hipGetLastError());
+}
+
+}  // namespace
+}  // namespace fa
+
+extern "C" int fa_kv_append(const fa_kvcache_args *args, void *stream) {
+    int rc = fa::check_kv(args);
+    if (rc || (rc = fa::check_append(*args))) return rc;
+    if (!fa::has_append(*args)) return FA_OK;
+    return fa::launch_prep(*args, true, false, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int fa_kv_splitkv(const fa_kvcache_args *args, void *stream) {
+    int rc = fa::check_kv(args);
+    if (rc || (rc = fa::check_split(*args))) return rc;
+    const fa_kvcache_args &a = *args;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (fa::split_items(a) == 0) return FA_OK;
+    if (a.batch_order && (rc = fa::launch_prep(a, false, true, s))) return rc;
+    return fa::launch_split(a, s);
+}
+
 extern "C" int fa_kv_combine(const fa_kvcache_args *args, void *stream) {
     int rc = fa::check_kv(args);
     if (rc) return rc;
     const fa_kvcache_args &a = *args;
-    if (a.num_splits <= 1) return FA_OK;
+    if (a.num_splits <= 1 || fa::fused_combine(a)) return FA_OK;
     if (!a.out_accum || !a.lse_accum) return FA_ERR_WORKSPACE;
-    const int64_t nrow = int64_t(a.batch) * a.nheads * a.seqlen_q;
-    if (nrow == 0) return FA_OK;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t blocks = (nrow + 3) / 4;
-    if (a.head_dim == 128)
-        hipLaunchKernelGGL(fa::kv_combine_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(fa::kv_combine_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, s, a);
-    return int(hipGetLastError());
+    return fa::launch_combine(a, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int fa_fwd_kvcache(const fa_kvcache_args *args, void *stream) {
-    int rc = fa_kv_append(args, stream);
-    if (rc) return rc;
-    rc = fa_kv_splitkv(args, stream);
-    if (rc) return rc;
-    return fa_kv_combine(args, stream);
+    int rc = fa::check_kv(args);
+    if (rc || (rc = fa::check_append(*args)) || (rc = fa::check_split(*args))) return rc;
+    const fa_kvcache_args &a = *args;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // One launch appends and ranks (the ranking reads cache_seqlens only).
+    const bool order = a.batch_order && fa::split_items(a) > 0;
+    if ((rc = fa::launch_prep(a, fa::has_append(a), order, s))) return rc;
+    if ((rc = fa::launch_split(a, s))) return rc;
+    return fa::launch_combine(a, s);
 }
 
 // ---------------------------------------------------------------------------
 // Allocation-free decode: fa_fwd_kvcache with its split workspace (out_accum,
-// lse_accum, batch_order) carved from a static device array instead of
-// caller memory, for callers that cannot allocate (code under HIP graph
-// capture, serving loops, harnesses that forbid hipMalloc).  The array is
-// FA_NOALLOC_SCRATCH_BYTES per device for the life of the process; its device
-// address is looked up once per device (hipGetSymbolAddress) and only that
-// address is handed to the kernels.  Nothing in it needs clearing between
+// lse_accum, batch_order, split_count) carved from a static device array
+// instead of caller memory, for callers that cannot allocate (code under HIP
+// graph capture, serving loops, harnesses that forbid hipMalloc).  The array
+// is FA_NOALLOC_SCRATCH_BYTES per device for the life of the process; its
+// device address is looked up once per device (hipGetSymbolAddress) and only
+// that address is handed to the kernels.  Nothing in it needs clearing between
 // calls: the split kernel writes every partial it later combines, and the
-// ordering kernel resets the work counter.  Calls on one device share the
-// array, so calls that overlap on a device (different streams) race.
+// ordering workgroup resets the work counter and the split counts.  Calls on
+// one device share the array, so calls that overlap on a device (different
+// streams) race.
 static __device__ __align__(256) char scratch[FA_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -783,9 +913,11 @@ int scratch_address(void **out) {
     return FA_OK;
 }
 
-// Scratch bytes a call needs: the split accumulators, then batch + 1 int32s of order and counter.
+// Scratch bytes a call needs: the split accumulators, then batch + 1 int32s of
+// order and counter, then the split counts.
 size_t noalloc_bytes(const fa_kvcache_args *a) {
-    return fa_kv_workspace_bytes(a) + (size_t(a->batch > 0 ? a->batch : 0) + 1) * sizeof(int32_t);
+    return fa_kv_workspace_bytes(a) +
+           (size_t(a->batch > 0 ? a->batch : 0) + 1 + size_t(fa_kv_split_count_len(a))) * sizeof(int32_t);
 }
 
 }  // namespace
@@ -806,5 +938,6 @@ extern "C" int fa_fwd_kvcache_noalloc(const fa_kvcache_args *args, void *stream)
         a.out_accum = a.lse_accum = nullptr;
     }
     a.batch_order = reinterpret_cast<int32_t *>(static_cast<char *>(base) + acc);
+    a.split_count = fa_kv_split_count_len(&a) > 0 ? a.batch_order + (a.batch > 0 ? a.batch : 0) + 1 : nullptr;
     return fa_fwd_kvcache(&a, stream);
 }

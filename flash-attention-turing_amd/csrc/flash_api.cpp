@@ -545,8 +545,6 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
     const bool options =
         a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
 
-    check_rc(fa_kv_append(&a, stream), "fa_kv_append");
-
     // Routing of flash_api.cpp:668: paged, explicit splits > 1 or single-token decode
     // take the split-KV kernel; a contiguous multi-token chunk takes the tiled
     // forward kernel with per-batch key counts and the batch remap.
@@ -556,19 +554,24 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
                                         int(batch_size), int(num_heads), int(num_heads_k),
                                         num_cus(q.get_device()));
         // Workspace: split accumulators (num_splits > 1), then the longest-first
-        // sequence order the split kernel schedules by and its work counter.
+        // sequence order the split kernel schedules by and its work counter, then
+        // the split counts with which it combines the partials itself.  Append,
+        // split and combine are then two launches.
         const int64_t rows = batch_size * num_heads * seqlen_q;
         const int64_t acc_floats = a.num_splits > 1 ? a.num_splits * rows * (head_size + 1) : 0;
-        at::Tensor ws = at::empty({acc_floats + batch_size + 1}, q.options().dtype(at::kFloat));
+        const int64_t counts = int64_t(fa_kv_split_count_len(&a));
+        at::Tensor ws = at::empty({acc_floats + batch_size + 1 + counts}, q.options().dtype(at::kFloat));
         if (a.num_splits > 1) {
             a.out_accum = ws.data_ptr<float>();
             a.lse_accum = a.out_accum + a.num_splits * rows * head_size;
         }
         a.batch_order = reinterpret_cast<int32_t *>(ws.data_ptr<float>() + acc_floats);
-        check_rc(fa_kv_splitkv(&a, stream), "fa_kv_splitkv");
-        check_rc(fa_kv_combine(&a, stream), "fa_kv_combine");
+        a.split_count = counts > 0 ? a.batch_order + batch_size + 1 : nullptr;
+        check_rc(fa_fwd_kvcache(&a, stream), "fa_fwd_kvcache");
         return {out, lse};
     }
+
+    check_rc(fa_kv_append(&a, stream), "fa_kv_append");
 
     fa_fwd_args f{};
     f.q = desc4(q);

@@ -71,7 +71,7 @@ class FaKvcacheArgs(ctypes.Structure):
         ("local_window", _i32), ("window_left", _i32), ("window_right", _i32), ("softcap", _f32),
         ("cache_leftpad", _p), ("alibi_slopes", _p), ("alibi_batch_stride", _i64),
         ("rotary_cos", _p), ("rotary_sin", _p), ("rotary_dim", _i32), ("rotary_seqlen", _i32),
-        ("rotary_interleaved", _i32),
+        ("rotary_interleaved", _i32), ("split_count", _p),
     ]
 
 
@@ -107,6 +107,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fa_kv_num_splits.restype = ctypes.c_int
     lib.fa_kv_workspace_bytes.argtypes = [ctypes.POINTER(FaKvcacheArgs)]
     lib.fa_kv_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_kv_split_count_len.argtypes = [ctypes.POINTER(FaKvcacheArgs)]
+    lib.fa_kv_split_count_len.restype = ctypes.c_size_t
     lib.fa_fwd_order_len.argtypes = [ctypes.POINTER(FaFwdArgs)]
     lib.fa_fwd_order_len.restype = ctypes.c_size_t
     lib.fa_bwd_order_len.argtypes = [ctypes.POINTER(FaBwdArgs)]
@@ -198,7 +200,7 @@ def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: floa
                  k_new=None, v_new=None, cache_batch_idx=None, block_table=None, out_accum=None,
                  lse_accum=None, batch_order=None, status=None, window=(-1, -1),
                  softcap: float = 0.0, cache_leftpad=None, alibi_slopes=None, rotary_cos=None, rotary_sin=None,
-                 rotary_interleaved: bool = True) -> FaKvcacheArgs:
+                 rotary_interleaved: bool = True, split_count=None) -> FaKvcacheArgs:
     a = FaKvcacheArgs()
     a.q, a.k_cache, a.v_cache, a.o = (tensor_desc(x) for x in (q, k_cache, v_cache, o))
     a.k_new, a.v_new = tensor_desc(k_new), tensor_desc(v_new)
@@ -227,6 +229,7 @@ def kvcache_args(q, k_cache, v_cache, o, lse, cache_seqlens, softmax_scale: floa
     a.rotary_dim = 0 if rotary_cos is None else 2 * rotary_cos.shape[1]
     a.rotary_seqlen = 0 if rotary_cos is None else rotary_cos.shape[0]
     a.rotary_interleaved = int(rotary_interleaved)
+    a.split_count = ptr(split_count)
     a._keep = (q, k_cache, v_cache, o, lse, cache_seqlens, k_new, v_new, cache_batch_idx, block_table, out_accum,
-               lse_accum, batch_order, status, cache_leftpad, alibi_slopes, rotary_cos, rotary_sin)
+               lse_accum, batch_order, status, cache_leftpad, alibi_slopes, rotary_cos, rotary_sin, split_count)
     return a

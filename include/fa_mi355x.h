@@ -150,8 +150,8 @@ typedef struct fa_kvcache_args {
     float *out_accum;               /* workspace [num_splits][batch*nheads*seqlen_q][d] fp32, 8-byte aligned */
     float *lse_accum;               /* workspace [num_splits][batch*nheads*seqlen_q] fp32    */
     int32_t *batch_order;           /* workspace [batch + 1]: sequences longest first and a work
-                                       counter (both filled by fa_kv_splitkv), or NULL for the
-                                       natural order                                           */
+                                       counter (both filled by fa_kv_splitkv or fa_fwd_kvcache),
+                                       or NULL for the natural order                           */
     /* Device-side input checks (replace the host reads of flash_api.cpp:627,
      * 634-641 and interface.py:855, so a decode step needs no host sync): a
      * sequence with cache_seqlens[b] < 0, cache_seqlens[b] + seqlen_new >
@@ -187,6 +187,13 @@ typedef struct fa_kvcache_args {
     int32_t rotary_dim;             /* 0: no rotary embedding                                       */
     int32_t rotary_seqlen;
     int32_t rotary_interleaved;
+    /* Workspace of fa_kv_split_count_len(args) int32s, or NULL.  With it, batch_order
+     * and num_splits > 1, the split kernel combines the partials itself: the last of
+     * the num_splits items of each (batch, kv head, 32-row tile) to finish reads them
+     * and writes o and lse, so fa_kv_combine has nothing left to do (it returns at
+     * once) and fa_fwd_kvcache runs two kernels (append with ordering, split) instead
+     * of four.  The ordering kernel zeroes these counts on every call. */
+    int32_t *split_count;
 } fa_kvcache_args;
 
 /* Split count for a request (kvcache_native.cu:913-952 choose_num_splits);
@@ -196,24 +203,31 @@ int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seq
 /* Bytes of the split accumulators for args->num_splits (0 when num_splits == 1);
  * batch_order, when used, needs (batch + 1) * 4 more. */
 size_t fa_kv_workspace_bytes(const fa_kvcache_args *args);
+/* int32s of the split_count workspace: batch * nheads_k * ceil(nheads / nheads_k *
+ * seqlen_q / 32) when num_splits > 1, else 0. */
+size_t fa_kv_split_count_len(const fa_kvcache_args *args);
 /* In-place append of k_new/v_new at cache_seqlens (contiguous, remapped or paged). */
 int fa_kv_append(const fa_kvcache_args *args, void *stream);
-/* Split-KV partial attention; writes o/lse directly when num_splits == 1. */
+/* Split-KV partial attention; writes o/lse directly when num_splits == 1, or with
+ * batch_order and split_count. */
 int fa_kv_splitkv(const fa_kvcache_args *args, void *stream);
-/* Log-sum-exp combine of the split partials into o/lse (kvcache_native.cu:676-729). */
+/* Log-sum-exp combine of the split partials into o/lse (kvcache_native.cu:676-729);
+ * nothing to do when fa_kv_splitkv combined them (batch_order and split_count set). */
 int fa_kv_combine(const fa_kvcache_args *args, void *stream);
-/* append + split-KV + combine in stream order. */
+/* append + split-KV + combine in stream order (with batch_order the append and the
+ * ordering share one launch). */
 int fa_fwd_kvcache(const fa_kvcache_args *args, void *stream);
 
 /*
  * Allocation-free variant of fa_fwd_kvcache.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
- * same kernels run; out_accum, lse_accum and batch_order in args are ignored
- * and taken instead from a static device array of FA_NOALLOC_SCRATCH_BYTES per
- * device, held until the process ends (the calling thread's current device
- * must be the stream's).  A request needing more than that, i.e.
- * fa_kv_workspace_bytes(args) + 4 * (batch + 1) bytes, returns FA_ERR_SCRATCH.
+ * same kernels run; out_accum, lse_accum, batch_order and split_count in args
+ * are ignored and taken instead from a static device array of
+ * FA_NOALLOC_SCRATCH_BYTES per device, held until the process ends (the calling
+ * thread's current device must be the stream's).  A request needing more than
+ * that, i.e. fa_kv_workspace_bytes(args) + 4 * (batch + 1 +
+ * fa_kv_split_count_len(args)) bytes, returns FA_ERR_SCRATCH.
  * No allocation or free happens in the call.  Calls on one device share its
  * array: calls that overlap on one device (on different streams) race.
  */

@@ -157,6 +157,16 @@ def test_validation_errors_before_any_launch(lib):
     assert ws(ctypes.byref(kv)) == 3 * 2 * 4 * 1 * (128 + 1) * 4
     kv.num_splits = 1
     assert ws(ctypes.byref(kv)) == 0
+    # Split counts: one per (batch, kv head, 32-row tile of the GQA group x query rows), with splits only.
+    cl = lib.fa_kv_split_count_len
+    cl.argtypes = [ctypes.POINTER(fa_capi.FaKvcacheArgs)]
+    cl.restype = ctypes.c_size_t
+    assert cl(ctypes.byref(kv)) == 0
+    kv.num_splits = 3
+    assert cl(ctypes.byref(kv)) == 2 * 2 * 1
+    kv.seqlen_q = 20  # 2 q-heads per kv head x 20 rows = 40 rows: two tiles
+    assert cl(ctypes.byref(kv)) == 2 * 2 * 2
+    kv.seqlen_q, kv.num_splits = 1, 1
     # Rotary: rotary_dim a multiple of 16 up to head_dim, both aligned tables,
     # at least one row, and new keys to rotate.
     kv.block_table, kv.page_block_size, kv.cache_batch_idx = None, 0, None

@@ -9,7 +9,9 @@ does not reach, against the oracle (through the ctypes binding, fa_capi):
   work item, no device work counter), plain and with the options instance;
 * a paged split whose keys span more than the 1024 page ids the split kernel
   stages in LDS: the fallback that reads the block table per tile
-  (the reference handles any length, kvcache_native.cu:1061-1062).
+  (the reference handles any length, kvcache_native.cu:1061-1062);
+* the split kernel's own combine (split counts), against the combine kernel
+  and the oracle.
 """
 
 import ctypes
@@ -101,8 +103,10 @@ def _kv_inputs(g, b, sq, h, hk, hd, cap, new, paged, page=256):
     return q, kc, vc, k, v, table
 
 
-def _kv_capi(device, q, kc, vc, k, v, seqlens, table, causal, splits, window=(-1, -1), order=False):
-    """fa_kv_append, fa_kv_splitkv, fa_kv_combine through the C ABI; batch_order only when ``order``."""
+def _kv_capi(device, q, kc, vc, k, v, seqlens, table, causal, splits, window=(-1, -1), order=False, fused=False,
+             calls=("fa_kv_append", "fa_kv_splitkv", "fa_kv_combine"), cache_batch_idx=None, status=None):
+    """The decode entry points ``calls`` through the C ABI; batch_order only when
+    ``order``, split counts (the split kernel's own combine) only when ``fused``."""
     qd, kcd, vcd = q.to(device), kc.clone().to(device), vc.clone().to(device)
     kd = None if k is None else k.to(device)
     vd = None if v is None else v.to(device)
@@ -112,13 +116,17 @@ def _kv_capi(device, q, kc, vc, k, v, seqlens, table, causal, splits, window=(-1
     rows = b * h * sq
     acc = torch.empty((splits * rows * (hd + 1),), dtype=torch.float32, device=device)
     border = torch.full((b + 1,), -3, dtype=torch.int32, device=device)
+    counts = torch.full((max(1, b * h * ((sq + 31) // 32)),), -3, dtype=torch.int32, device=device)
     a = fa_capi.kvcache_args(qd, kcd, vcd, o, lse, seqlens.to(device), hd ** -0.5, causal, splits, kd, vd,
                              block_table=None if table is None else table.to(device),
+                             cache_batch_idx=None if cache_batch_idx is None else cache_batch_idx.to(device),
                              out_accum=acc if splits > 1 else None,
                              lse_accum=acc[splits * rows * hd:] if splits > 1 else None,
-                             batch_order=border if order else None, window=window)
+                             batch_order=border if order else None, window=window,
+                             split_count=counts if fused else None, status=status)
     assert fa_capi.load().fa_kv_workspace_bytes(ctypes.byref(a)) <= acc.numel() * 4
-    for name in ("fa_kv_append", "fa_kv_splitkv", "fa_kv_combine"):
+    assert fa_capi.load().fa_kv_split_count_len(ctypes.byref(a)) <= counts.numel()
+    for name in calls:
         fa_capi.call(name, a)
     torch.cuda.synchronize()
     return o.cpu(), lse.cpu(), kcd.cpu(), vcd.cpu()
@@ -151,6 +159,63 @@ def test_splitkv_natural_order(device, b, sq, h, hk, hd, cap, new, paged, splits
     # Same bits as the longest-first resident grid (the order does not change any item's arithmetic).
     got = _kv_capi(device, q, kc, vc, k, v, seqlens, table, True, splits, window, order=True)
     assert torch.equal(got[0], out) and torch.equal(got[1], lse)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,sq,h,hk,hd,cap,new,paged,splits,window,remap", [
+    (7, 1, 32, 8, 128, 2048, 1, True, 8, (-1, -1), False),   # c4's form: GQA group of 4 rows, paged
+    (4, 4, 16, 16, 64, 4096, 4, False, 16, (-1, -1), True),  # c5's form: MHA, 4 query rows, remapped
+    (3, 5, 16, 2, 128, 1024, 5, False, 3, (-1, -1), False),  # 40 rows of a kv head: two row tiles
+    (5, 2, 8, 2, 64, 768, 2, True, 5, (200, -1), False),     # options instance (local window)
+])
+def test_fused_combine(device, b, sq, h, hk, hd, cap, new, paged, splits, window, remap):
+    """With batch_order and split counts the split kernel combines its partials
+    itself (the last split item of each row tile to finish) and fa_fwd_kvcache
+    is two launches: the same bits as the combine kernel, the oracle's values,
+    and a second call right after (other lengths) starts from counts the
+    ordering workgroup zeroed again.  An invalid sequence (cache overflow) is
+    reported and gets O = 0, LSE = 0 through the fused path too."""
+    g = torch.Generator().manual_seed(9250 + b + sq + hd + splits)
+    q, kc, vc, k, v, table = _kv_inputs(g, b, sq, h, hk, hd, cap, new, paged)
+    rows_c = b + 2 if remap else b
+    if remap:
+        kc = torch.cat([kc, randn16((2,) + tuple(kc.shape[1:]), g)])
+        vc = torch.cat([vc, randn16((2,) + tuple(vc.shape[1:]), g)])
+    idx = torch.randperm(rows_c, generator=g)[:b].to(torch.int32) if remap else None
+    for call in range(2):
+        seqlens = torch.randint(0, cap - new + 1, (b,), generator=g, dtype=torch.int32)
+        seqlens[call] = cap - new
+        seqlens[-1] = cap - new + 1  # overflows the cache after the append: invalid
+        print(f"case fused b={b} sq={sq} hd={hd} splits={splits} call={call}", flush=True)
+        st_f = torch.zeros(1, dtype=torch.int32, device=device)
+        ref = _kv_capi(device, q, kc, vc, k, v, seqlens, table, True, splits, window, order=True,
+                       cache_batch_idx=idx)
+        got = _kv_capi(device, q, kc, vc, k, v, seqlens, table, True, splits, window, order=True, fused=True,
+                       calls=("fa_fwd_kvcache",), cache_batch_idx=idx, status=st_f)
+        for n, r, x in zip(("out", "lse", "k_cache", "v_cache"), ref, got):
+            assert torch.equal(r, x), f"{n}: fused combine differs from the combine kernel"
+        # The three entry points with counts: fa_kv_splitkv combines, fa_kv_combine has nothing left to do.
+        three = _kv_capi(device, q, kc, vc, k, v, seqlens, table, True, splits, window, order=True, fused=True,
+                         cache_batch_idx=idx)
+        assert torch.equal(three[0], ref[0]) and torch.equal(three[1], ref[1])
+        assert int(st_f.item()) == 1, "the overflowing sequence is reported"
+        out, lse = got[0], got[1]
+        assert not out[-1].any() and not lse[-1].any(), "an invalid sequence gets O = 0, LSE = 0"
+        valid = slice(0, b - 1)
+        sl = seqlens[valid]
+        kcv, vcv = (kc, vc)
+        kv_idx = None if idx is None else idx[valid]
+        tab = None if table is None else table[valid]
+        if window == (-1, -1):
+            o_ref, l_ref, _, _ = kv_oracle(q[valid], kcv, vcv, k[valid], v[valid], sl, kv_idx, tab, True, splits,
+                                           None)
+        else:
+            _, _, kc_ref, vc_ref = kv_oracle(q[valid], kcv, vcv, k[valid], v[valid], sl, kv_idx, tab, True, splits,
+                                             None)
+            ku, vu = okv.materialize(kc_ref, vc_ref, sl + new, kv_idx, tab)
+            o_ref, l_ref = okv.splitkv_attention(q[valid], ku, vu, sl + new, hd ** -0.5, True, splits, window=window)
+        assert_2x("out", out[valid], o_ref, o_ref.to(torch.float16))
+        assert_lse(lse[valid], l_ref)
 
 
 @pytest.mark.gpu

@@ -37,14 +37,17 @@ def _call(device, name, inp, splits, workspace):
     b, sq, h, hd = q.shape
     lse = torch.full((b, h, sq), 3.0, dtype=torch.float32, device=device)
     rows = b * h * sq
-    acc = oa = la = order = None
+    acc = oa = la = order = counts = None
     if workspace:
         acc = torch.empty((max(splits, 1) * rows * (hd + 1),), dtype=torch.float32, device=device)
         oa, la = (acc, acc[splits * rows * hd:]) if splits > 1 else (None, None)
         order = torch.empty((b + 1,), dtype=torch.int32, device=device)
+        counts = torch.empty((b * h * ((sq + 31) // 32),), dtype=torch.int32, device=device)
     a = fa_capi.kvcache_args(qd, kcd, vcd, o, lse, lens.to(device), hd ** -0.5, True, splits, kd, vd,
                              block_table=None if table is None else table.to(device), out_accum=oa, lse_accum=la,
-                             batch_order=order)
+                             batch_order=order, split_count=counts)
+    if workspace:
+        assert fa_capi.load().fa_kv_split_count_len(ctypes.byref(a)) <= counts.numel()
     print(f"{name}: b={b} sq={sq} h={h} hd={hd} splits={splits}", flush=True)
     fa_capi.call(name, a)
     torch.cuda.synchronize()
