@@ -140,7 +140,7 @@ def test_fwd_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, h
         res[ordered] = (o.cpu(), lse.cpu())
         if ordered:
             cus = torch.cuda.get_device_properties(0).multi_processor_count
-            bm = 256 if hd == 128 and ((mq + 255) // 256) * len(lens_q) * h >= 2 * cus else 128
+            bm = 256 if hd == 128 and ((mq + 255) // 256) * len(lens_q) * h >= 2 * cus and mq >= 2048 else 128
             nmb = (mq + bm - 1) // bm
             got = order.cpu().tolist()[: len(lens_q) * nmb]
             assert sorted(got) == list(range(len(lens_q) * nmb)), "every item exactly once"

@@ -55,6 +55,31 @@ def test_fwd_parity(device, hd, causal, sq, sk, heads, batch, scale):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("causal,sq,sk", [(False, 2300, 2300), (True, 2100, 3000), (False, 2048, 1500),
+                                          (True, 2400, 2400)])
+def test_fwd_pingpong_shapes(device, causal, sq, sk):
+    """Shapes on which fa_fwd takes the ping-pong kernel (head_dim 128, at least
+    2048 query rows and a grid of 256-row blocks at least twice the CU count):
+    non-causal, ragged ends, sq != sk both ways, GQA 16 / 4.  Batch row 0 of
+    every head against the oracle (the whole batch runs on the GPU)."""
+    b, h, hk, hd = 4, 16, 4, 128
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert sq >= 2048 and ((sq + 255) // 256) * b * h >= 2 * cus, "shape must select the ping-pong kernel"
+    g = torch.Generator().manual_seed(1500 + sq + sk + int(causal))
+    q = randn16((b, sq, h, hd), g)
+    k = randn16((b, sk, hk, hd), g)
+    v = randn16((b, sk, hk, hd), g)
+    s = hd ** -0.5
+    print(f"case pingpong causal={causal} sq={sq} sk={sk}", flush=True)
+    out, lse = fai._flash_attn_forward(q.to(device), k.to(device), v.to(device), s, causal)
+    torch.cuda.synchronize()
+    o_ref, l_ref = attention_fwd(q[:1], k[:1], v[:1], s, causal)
+    o_twin, _ = fwd_twin(q[:1], k[:1], v[:1], s, causal)
+    assert_2x("out", out[:1].cpu(), o_ref, o_twin)
+    assert_lse(lse[:1].cpu(), l_ref)
+
+
+@pytest.mark.gpu
 def test_fwd_fully_masked_rows(device):
     """Causal with sq > sk: the first sq - sk rows see no key -> O = 0, LSE = 0
     (flash_fwd_kernel.h:616-662)."""
