@@ -158,8 +158,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         char *ks = smem + st * C::STAGE;
         const int n0 = nb * BN;
         if (n0 + BN <= sk) {
-            kcp.copy_to(lds_addr(smem) + st * C::STAGE, kp + int64_t(n0) * krs, krs);
-            vcp.copy_to(lds_addr(smem) + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
+            // Addresses formed per call: hoisted, they were spilled at head_dim 128.
+            kcp.template copy_to<true>(lds_addr(smem) + st * C::STAGE, kp + int64_t(n0) * krs, krs);
+            vcp.template copy_to<true>(lds_addr(smem) + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
         } else {
             dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
             dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
@@ -215,7 +216,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     for (int nb = n_full; nb < n_blocks; ++nb) block(nb, std::true_type{});
 
     if (qv) {
-        f16 *row = dqp + int64_t(qi) * a.dq.row_stride;
+        // Opaque to the optimiser: keeps the output address from being computed
+        // before the block loops and held (spilled) through them.
+        int qo = qi;
+        asm volatile("" : "+v"(qo));
+        f16 *row = dqp + int64_t(qo) * a.dq.row_stride;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll

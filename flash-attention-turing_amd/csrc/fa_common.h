@@ -249,14 +249,20 @@ struct TileCopier {
         copy_to(lds_addr(tile), src_row0, rs);
     }
     // The same with the tile given as its LDS byte address (no pointer cast in the loop).
+    // FRESH: the per-copy lane addresses are formed on every call (one 64-bit add
+    // each; the offset is opaque to the optimiser) instead of being hoisted out
+    // of the caller's loop as CPT loop-invariant pointers held in registers.
+    template <bool FRESH = false>
     __device__ __forceinline__ void copy_to(uint32_t tile_l, const f16 *src_row0, int64_t rs) const {
         const uint32_t l0 = __builtin_amdgcn_readfirstlane(tile_l + lds0);
+        int64_t go = goff;
+        if constexpr (FRESH) asm volatile("" : "+v"(go));
         if constexpr (CPT == 1 || CPT == 2 || CPT == 4) {
             const void *g[CPT];
             uint32_t l[CPT];
 #pragma unroll
             for (int i = 0; i < CPT; ++i) {
-                g[i] = src_row0 + goff + int64_t(i) * RSTEP * rs;
+                g[i] = src_row0 + go + int64_t(i) * RSTEP * rs;
                 l[i] = l0 + i * WAVES * 1024;
             }
             g2l16_batch<CPT>(g, l);

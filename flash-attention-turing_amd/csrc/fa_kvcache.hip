@@ -457,7 +457,11 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         const bool pages_in_lds = n_pages <= C::MAX_PAGES;
         if (a.block_table && pages_in_lds) {
             const int32_t *bt = a.block_table + int64_t(b) * a.block_table_stride + pg_first;
-            for (int i = tid; i < n_pages; i += kKvThreads) pages[i] = bt[i];
+            // Opaque start index: keeps this loop's per-lane addresses from being
+            // hoisted out of the item loop (and spilled in the options instance).
+            int i0 = tid;
+            asm volatile("" : "+v"(i0));
+            for (int i = i0; i < n_pages; i += kKvThreads) pages[i] = bt[i];
         }
         __syncthreads();
 
