@@ -717,7 +717,10 @@ extern "C" int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_d
     // streams best with about 8192 cache positions: fewer and the per-item
     // start-up and the combine weigh in, more and the longest-first deal
     // balances worse.  Enough splits are also taken for one item per compute
-    // unit, and a split keeps at least 512 positions.  Only the capacity is
+    // unit, and a split keeps at least 512 positions, or, for a cache of 512
+    // positions or more cut into at most 16 splits, at least 64 (a short cache
+    // on few sequences: one sequence of 1024 positions, 32 / 8 heads, takes
+    // 15.5 us per call in 16 splits against 20.3 in 2).  Only the capacity is
     // known on the host (the live lengths are on the device).
     (void)head_dim;
     if (requested > 0) return requested;
@@ -726,7 +729,9 @@ extern "C" int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_d
     const int64_t wgs = int64_t(batch) * nheads_k * ((rows + 31) / 32);
     const int64_t by_len = (int64_t(seqlen_k_capacity) + 4096) / 8192;
     const int64_t by_fill = (int64_t(std::max(num_cus, 1)) + wgs - 1) / std::max<int64_t>(wgs, 1);
-    const int64_t max_by_len = std::max(1, seqlen_k_capacity / 512);
+    int64_t max_by_len = seqlen_k_capacity / 512;
+    if (seqlen_k_capacity >= 512) max_by_len = std::max<int64_t>(max_by_len, std::min(16, seqlen_k_capacity / 64));
+    max_by_len = std::max<int64_t>(1, max_by_len);
     return int(std::max<int64_t>(1, std::min<int64_t>({std::max(by_len, by_fill), max_by_len, 128})));
 }
 

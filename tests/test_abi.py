@@ -63,6 +63,10 @@ def test_num_splits_heuristic(lib):
         (131072 + 256, 128, 1, 1, 32, 8): 32,  # 1 x 128k
         (131072, 64, 4, 4, 16, 16): 16,        # c5: 4 query tokens, 65k-131k
         (8192, 128, 1, 16, 32, 8): 2,          # 16 x 8k
+        (2048, 128, 1, 1, 32, 8): 16,          # short caches on few sequences: down to 64-128 positions
+        (1024, 128, 1, 1, 32, 8): 16,
+        (512, 128, 1, 1, 32, 8): 8,
+        (2048, 128, 1, 4, 32, 8): 8,
     }
     for (cap, d, sq, b, h, hk), best in measured_best.items():
         assert f(0, cap, d, sq, b, h, hk, 256) == best
