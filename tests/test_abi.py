@@ -103,6 +103,43 @@ def test_ctypes_structs_match_the_c_layout(tmp_path):
         assert int(value) == expect, f"{cname}.{field}: C {value} vs ctypes {expect}"
 
 
+def test_c_program_links_the_library(tmp_path):
+    """A plain C caller: compiled against include/fa_mi355x.h with gcc, linked
+    with -lfa_mi355x, it calls the host-only entry points (argument checks,
+    sizes, the split heuristic, error texts) with no GPU work."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "caller.c"
+    src.write_text(r"""
+#include <stdio.h>
+#include <string.h>
+#include "fa_mi355x.h"
+int main(void) {
+    fa_kvcache_args kv;
+    memset(&kv, 0, sizeof kv);
+    kv.batch = 2; kv.seqlen_q = 20; kv.nheads = 4; kv.nheads_k = 2; kv.head_dim = 128; kv.num_splits = 3;
+    printf("%d %d %d\n", fa_fwd(NULL, NULL), fa_bwd(NULL, NULL), fa_fwd_kvcache(NULL, NULL));
+    printf("%zu %zu\n", fa_kv_workspace_bytes(&kv), fa_kv_split_count_len(&kv));
+    printf("%d\n", fa_kv_num_splits(0, 32768 + 256, 128, 1, 64, 32, 8, 256));
+    printf("%s\n", fa_error_string(FA_ERR_WORKSPACE));
+    return 0;
+}
+""")
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(LIB)
+    rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+    subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe), f"-L{libdir}",
+                    "-lfa_mi355x", f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{rocm_lib}"], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    assert out[0].split() == ["-1", "-1", "-1"]
+    assert out[1].split() == [str(3 * 2 * 4 * 20 * 129 * 4), str(2 * 2 * 2)]
+    assert out[2] == "4"
+    assert "workspace" in out[3]
+
+
 def _capi():
     import sys
 
