@@ -123,6 +123,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     const int n_blocks = (n_end + BN - 1) / BN;
     const float cs = a.softmax_scale * kLog2e;
 
+    TileCopier<HD, BN, NT> kcp, vcp;
+    kcp.init(krs, wave, lane);
+    vcp.init(vrs, wave, lane);
+    auto issue = [&](int nb, int st) {
+        char *ks = smem + st * C::STAGE;
+        const int n0 = nb * BN;
+        if (n0 + BN <= sk) {
+            // Addresses formed per call: hoisted, they were spilled at head_dim 128.
+            kcp.template copy_to<true>(lds_addr(smem) + st * C::STAGE, kp + int64_t(n0) * krs, krs);
+            vcp.template copy_to<true>(lds_addr(smem) + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
+        } else {
+            dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
+            dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
+        }
+    };
+    // Block 0's copies go out before the row loads below, so the two
+    // latencies overlap; the first block's wait covers both.
+    if (n_blocks > 0) issue(0, 0);
+
     // Q^T, dO^T as B operands (lane: query col, d = 16g + 8hh + 0..7) and this
     // lane's half of D = sum_d O * dO.
     const int qi = m0 + wave * 32 + col;
@@ -143,7 +162,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         a.dsum[lrow + qi] = -dsum;  // -D: the dK/dV kernel seeds its dP accumulators with it
         a.dsum[int64_t(a.batch) * a.nheads * a.lse_seqlen + lrow + qi] = lse2;  // for the dK/dV kernel
     }
-    wait_vmem();  // only the tile copies are in flight inside the loop
 
     f32x16 dq[HD / 32];
 #pragma unroll
@@ -151,21 +169,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 
     TileReader<HD> rd;
     rd.init(lane);
-    TileCopier<HD, BN, NT> kcp, vcp;
-    kcp.init(krs, wave, lane);
-    vcp.init(vrs, wave, lane);
-    auto issue = [&](int nb, int st) {
-        char *ks = smem + st * C::STAGE;
-        const int n0 = nb * BN;
-        if (n0 + BN <= sk) {
-            // Addresses formed per call: hoisted, they were spilled at head_dim 128.
-            kcp.template copy_to<true>(lds_addr(smem) + st * C::STAGE, kp + int64_t(n0) * krs, krs);
-            vcp.template copy_to<true>(lds_addr(smem) + st * C::STAGE + C::TILE, vp + int64_t(n0) * vrs, vrs);
-        } else {
-            dma_tile<HD, BN, NT>(ks, kp, krs, n0, sk - 1, wave, lane);
-            dma_tile<HD, BN, NT>(ks + C::TILE, vp, vrs, n0, sk - 1, wave, lane);
-        }
-    };
 
     const int q_lo = m0 + wave * 32;
     auto block = [&](int nb, auto mask_tag) {
@@ -211,7 +214,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     // Blocks [0, n_full) are fully visible to every row of the workgroup.
     int n_full = min(n_blocks, sk / BN);
     if (CAUSAL) n_full = min(n_full, max(0, (m0 + causal_off + 1) / BN));
-    if (n_blocks > 0) issue(0, 0);
     for (int nb = 0; nb < n_full; ++nb) block(nb, std::false_type{});
     for (int nb = n_full; nb < n_blocks; ++nb) block(nb, std::true_type{});
 
