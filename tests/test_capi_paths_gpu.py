@@ -167,6 +167,7 @@ def test_splitkv_natural_order(device, b, sq, h, hk, hd, cap, new, paged, splits
     (4, 4, 16, 16, 64, 4096, 4, False, 16, (-1, -1), True),  # c5's form: MHA, 4 query rows, remapped
     (3, 5, 16, 2, 128, 1024, 5, False, 3, (-1, -1), False),  # 40 rows of a kv head: two row tiles
     (5, 2, 8, 2, 64, 768, 2, True, 5, (200, -1), False),     # options instance (local window)
+    (3, 3, 32, 1, 64, 1024, 3, False, 70, (-1, -1), False),   # 96 rows (three tiles), 70 splits (> 64)
 ])
 def test_fused_combine(device, b, sq, h, hk, hd, cap, new, paged, splits, window, remap):
     """With batch_order and split counts the split kernel combines its partials
