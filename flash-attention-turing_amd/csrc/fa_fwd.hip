@@ -66,9 +66,13 @@ __device__ __forceinline__ float sum8(const f16x8 &v, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
 }
 
-// Per-workgroup extents and base pointers of one (batch, head, query block).
+// Per-workgroup extents and base pointers of one (batch, query heads, block of
+// query positions).  A workgroup covers gp = 2^lg query heads of one GQA group
+// (gp divides the group, so the heads share their K / V) at P = BM / gp
+// positions from m0: its K / V tiles serve all of them.  Each wave takes 32
+// rows of one head (fwd_wave narrows the pointers to it).
 struct FwdWork {
-    int b, h, hk, sq, sk, m0, causal_off, n_blocks;
+    int b, h, hk, sq, sk, m0, P, causal_off, n_blocks;
     const f16 *qp, *kp, *vp;
     f16 *op;
     float *lse_row;
@@ -79,22 +83,25 @@ struct FwdWork {
 // Fills w for workgroup blockIdx.x; false when the block has no query rows
 // (its LSE padding is then written here).
 template <int BM, bool CAUSAL>
-__device__ __forceinline__ bool fwd_work(const fa_fwd_args &a, int num_m_blocks, FwdWork &w) {
+__device__ __forceinline__ bool fwd_work(const fa_fwd_args &a, int num_m_blocks, int lg, FwdWork &w) {
     int mb;
+    const int gp = 1 << lg;
+    const int packs = a.nheads >> lg;  // head packs per batch
     if (a.work_order && a.cu_seqlens_q) {
-        // Item of the device-built order (heads fastest), longest first.
-        const int it = a.work_order[blockIdx.x / a.nheads];
+        // Item of the device-built order (head packs fastest), longest first.
+        const int it = a.work_order[blockIdx.x / packs];
         w.b = __builtin_amdgcn_readfirstlane(it / num_m_blocks);
         mb = __builtin_amdgcn_readfirstlane(it - w.b * num_m_blocks);
-        w.h = blockIdx.x % a.nheads;
+        w.h = (blockIdx.x % packs) * gp;
     } else {
-        const int bh_count = a.batch * a.nheads;
-        const int bh = blockIdx.x % bh_count;
-        mb = blockIdx.x / bh_count;
+        const int bp_count = a.batch * packs;
+        const int bp = blockIdx.x % bp_count;
+        mb = blockIdx.x / bp_count;
         if (CAUSAL) mb = num_m_blocks - 1 - mb;  // causal blocks are issued heaviest first
-        w.b = bh / a.nheads;
-        w.h = bh - w.b * a.nheads;
+        w.b = bp / packs;
+        w.h = (bp - w.b * packs) * gp;
     }
+    w.P = BM >> lg;
     w.hk = w.h / (a.nheads / a.nheads_k);
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
     const SeqInfo si = seq_info(w.b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, a.seqused_k,
@@ -114,11 +121,14 @@ __device__ __forceinline__ bool fwd_work(const fa_fwd_args &a, int num_m_blocks,
             if (a.status && threadIdx.x == 0) atomicOr(a.status, err);
         }
     }
-    w.m0 = mb * BM;
+    w.m0 = mb * w.P;
     w.lse_row = a.lse + (int64_t(w.b) * a.nheads + w.h) * a.lse_seqlen;
     if (w.m0 >= w.sq) {
         // Rows past this sequence's length: LSE padding is 0 (flash_api.cpp:388).
-        for (int i = w.m0 + threadIdx.x; i < w.m0 + BM && i < a.lse_seqlen; i += blockDim.x) w.lse_row[i] = 0.f;
+        for (int i = threadIdx.x; i < gp * w.P; i += blockDim.x) {
+            const int row = w.m0 + i % w.P;
+            if (row < a.lse_seqlen) w.lse_row[int64_t(i / w.P) * a.lse_seqlen + row] = 0.f;
+        }
         return false;
     }
     w.qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, w.b, si.q_start, w.h);
@@ -127,12 +137,25 @@ __device__ __forceinline__ bool fwd_work(const fa_fwd_args &a, int num_m_blocks,
     w.op = (f16 *)a.o.ptr + base_off(a.o, packed_q, w.b, si.q_start, w.h);
     w.causal_off = w.sk - w.sq;  // key j visible to query i iff j <= i + causal_off
     int n_end = w.sk;
-    if (CAUSAL) n_end = max(0, min(w.sk, w.m0 + BM + w.causal_off));
+    if (CAUSAL) n_end = max(0, min(w.sk, w.m0 + w.P + w.causal_off));
     w.n_blocks = (n_end + kFwdBN - 1) / kFwdBN;
     // Negative scales are folded into Q's sign so that the exp argument uses |scale|.
     w.neg = a.softmax_scale < 0.f;
     w.cscale = fabsf(a.softmax_scale) * kLog2e;
     return true;
+}
+
+// Narrows w to the rows of 32-row tile t of the workgroup: tile t is head
+// w.h + t / (P / 32), positions m0 + 32 (t % (P / 32)) .. + 31.  Returns the
+// tile's first position.
+__device__ __forceinline__ int fwd_wave(const fa_fwd_args &a, FwdWork &w, int t) {
+    const int tiles = w.P >> 5;  // position tiles per head (a power of two)
+    const int hp = t >> (31 - __builtin_clz(tiles));
+    w.h += hp;
+    w.qp += int64_t(hp) * a.q.head_stride;
+    w.op += int64_t(hp) * a.o.head_stride;
+    w.lse_row += int64_t(hp) * a.lse_seqlen;
+    return w.m0 + 32 * (t & (tiles - 1));
 }
 
 // Q^T of query qi as B operands: lane (query col, half hh), K step g covers d = 16g + 8hh + 0..7.
@@ -261,7 +284,7 @@ struct KvLoader {
 // workgroups per CU (64 KB LDS each at head_dim 128) overlap one wave's
 // softmax with the other's MFMAs on each SIMD.
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks) {
+__global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks, const int lg) {
     constexpr int NT = 256;
     using C = FwdCfg<HD, NT>;
     constexpr int BM = C::BM, BN = C::BN;
@@ -271,9 +294,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int hh = lane >> 5;
     FwdWork w;
-    if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, w)) return;
+    if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, lg, w)) return;
 
-    const int q_lo = w.m0 + wave * 32;
+    const int q_lo = fwd_wave(a, w, wave);
     const int qi = q_lo + (lane & 31);
     f16x8 qB[HD / 16];
     load_q<HD>(a, w, qi, hh, qB);
@@ -346,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
 constexpr int kPpPipe = 8;
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, const int num_m_blocks) {
+__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, const int num_m_blocks, const int lg) {
     constexpr int NT = 512;
     using C = FwdCfg<HD, NT>;
     constexpr int BM = C::BM, BN = C::BN;
@@ -357,9 +380,9 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, con
     const int grp = wave >> 2;                                  // 0: matrix phase first
     const int hh = lane >> 5;
     FwdWork w;
-    if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, w)) return;
+    if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, lg, w)) return;
 
-    const int q_lo = w.m0 + (2 * (wave & 3) + grp) * 32;
+    const int q_lo = fwd_wave(a, w, 2 * (wave & 3) + grp);
     const int qi = q_lo + (lane & 31);
     f16x8 qB[HD / 16];
     load_q<HD>(a, w, qi, hh, qB);
@@ -503,28 +526,38 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, con
 }
 
 // Varlen work order (order_items in fa_common.h): item it = b * nmb + mb is
-// query block mb (BM rows) of sequence b, its work about rows x keys seen by
-// the block's last row, in buckets of BM x 64; blocks past a sequence's end
-// come last (they still write LSE padding).
-template <int BM>
-__global__ __launch_bounds__(kOrderThreads) void fwd_order_kernel(const fa_fwd_args a, const int nmb) {
+// block mb of P query positions of sequence b, its work about positions x
+// keys seen by the block's last position, in buckets of P x 64; blocks past a
+// sequence's end come last (they still write LSE padding).
+__global__ __launch_bounds__(kOrderThreads) void fwd_order_kernel(const fa_fwd_args a, const int nmb, const int P) {
     order_items(a.batch * nmb, [&](int it) {
         const int b = it / nmb, mb = it - b * nmb;
         const int sq = a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b];
         const int sk = a.cu_seqlens_k ? a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b] : a.seqlen_k;
-        const int m0 = mb * BM;
+        const int m0 = mb * P;
         if (m0 >= sq) return -1;
-        const int64_t rows = min(BM, sq - m0);
-        const int64_t keys = a.causal ? max(0, min(sk, m0 + BM + sk - sq)) : max(sk, 0);
-        return int(min<int64_t>(rows * keys / (BM * 64), kOrderBuckets - 1));
+        const int64_t rows = min(P, sq - m0);
+        const int64_t keys = a.causal ? max(0, min(sk, m0 + P + sk - sq)) : max(sk, 0);
+        return int(min<int64_t>(rows * keys / (int64_t(P) * 64), kOrderBuckets - 1));
     }, a.work_order, true);
 }
 
-template <int BM>
-static int launch_order(const fa_fwd_args &a, int nmb, hipStream_t stream) {
+static int launch_order(const fa_fwd_args &a, int nmb, int P, hipStream_t stream) {
     if (!a.work_order || !a.cu_seqlens_q) return FA_OK;
-    hipLaunchKernelGGL(fwd_order_kernel<BM>, dim3(1), dim3(kOrderThreads), 0, stream, a, nmb);
+    hipLaunchKernelGGL(fwd_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, a, nmb, P);
     return int(hipGetLastError());
+}
+
+// log2 of the query heads per workgroup for a BM-row kernel: the largest
+// power of two that divides the GQA group (those heads read the same K / V)
+// and leaves whole 32-row tiles per head.  The K / V tiles a workgroup loads
+// then serve gp heads instead of one, and the workgroup spans BM / gp
+// positions, so a causal block wastes less on the diagonal.
+static int fwd_pack_log2(const fa_fwd_args &a, int BM) {
+    const int group = a.nheads / a.nheads_k;
+    int lg = 0;
+    while ((64 << lg) <= BM && group % (2 << lg) == 0) ++lg;
+    return lg;
 }
 
 template <int HD, bool CAUSAL>
@@ -537,24 +570,28 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
     // +3 %, 64 x U[64, 1024] +14 %; 32 x 2048 even; 16 x 4096 -5 %).  Both
     // give the same bits.
     if constexpr (HD == 128) {
-        const int64_t pp_m_blocks = (a.lse_seqlen + FwdCfg<HD, 512>::BM - 1) / FwdCfg<HD, 512>::BM;
-        const int64_t pp_grid = pp_m_blocks * a.batch * a.nheads;
+        constexpr int BM = FwdCfg<HD, 512>::BM;
+        const int lg = fwd_pack_log2(a, BM), P = BM >> lg;
+        const int64_t pp_m_blocks = (a.lse_seqlen + P - 1) / P;
+        const int64_t pp_grid = pp_m_blocks * a.batch * (a.nheads >> lg);
         if (pp_grid >= 2 * int64_t(device_cus()) && a.lse_seqlen >= 2048) {
             if (pp_grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
-            const int rc = launch_order<FwdCfg<HD, 512>::BM>(a, int(pp_m_blocks), stream);
+            const int rc = launch_order(a, int(pp_m_blocks), P, stream);
             if (rc) return rc;
             hipLaunchKernelGGL((fwd_pp_kernel<HD, CAUSAL>), dim3(unsigned(pp_grid)), dim3(512), 0, stream, a,
-                               int(pp_m_blocks));
+                               int(pp_m_blocks), lg);
             return int(hipGetLastError());
         }
     }
-    const int num_m_blocks = (a.lse_seqlen + FwdCfg<HD, 256>::BM - 1) / FwdCfg<HD, 256>::BM;
-    const int64_t grid = int64_t(num_m_blocks) * a.batch * a.nheads;
+    constexpr int BM = FwdCfg<HD, 256>::BM;
+    const int lg = fwd_pack_log2(a, BM), P = BM >> lg;
+    const int num_m_blocks = (a.lse_seqlen + P - 1) / P;
+    const int64_t grid = int64_t(num_m_blocks) * a.batch * (a.nheads >> lg);
     if (grid == 0) return FA_OK;
     if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
-    const int rc = launch_order<FwdCfg<HD, 256>::BM>(a, num_m_blocks, stream);
+    const int rc = launch_order(a, num_m_blocks, P, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(256), 0, stream, a, num_m_blocks);
+    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(256), 0, stream, a, num_m_blocks, lg);
     return int(hipGetLastError());
 }
 
@@ -580,5 +617,5 @@ extern "C" int fa_fwd(const fa_fwd_args *args, void *stream) {
 
 extern "C" size_t fa_fwd_order_len(const fa_fwd_args *a) {
     if (!a || a->batch <= 0 || a->lse_seqlen <= 0) return 0;
-    return size_t(a->batch) * size_t((a->lse_seqlen + 127) / 128);
+    return size_t(a->batch) * size_t((a->lse_seqlen + 31) / 32);  // blocks of 32 positions at the least
 }

@@ -76,7 +76,7 @@ typedef struct fa_fwd_args {
     int32_t *work_order;
 } fa_fwd_args;
 
-/* Length in int32s of fa_fwd's work_order workspace: batch * ceil(lse_seqlen / 128).
+/* Length in int32s of fa_fwd's work_order workspace: batch * ceil(lse_seqlen / 32).
  * No counterpart in the reference (its grid is in natural order). */
 size_t fa_fwd_order_len(const fa_fwd_args *args);
 int fa_fwd(const fa_fwd_args *args, void *stream);

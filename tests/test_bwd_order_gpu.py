@@ -100,6 +100,15 @@ def test_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, hd, c
                  causal)
 
 
+def _fwd_pack(h, hk, bm):
+    """Query heads per forward workgroup: the largest power of two dividing
+    the GQA group that leaves whole 32-row tiles per head."""
+    gp = 1
+    while 2 * gp <= bm // 32 and (h // hk) % (2 * gp) == 0:
+        gp *= 2
+    return gp
+
+
 def _fwd_bucket(lq, lk, mb, bm, causal):
     m0 = bm * mb
     if m0 >= lq:
@@ -130,7 +139,7 @@ def test_fwd_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, h
         lse = torch.full((len(lens_q), h, mq), 7.0, dtype=torch.float32, device=device)
         fa = fa_capi.fwd_args(q, k, v, o, lse, s, causal, cq, ck, mq, mk)
         n = fa_capi.load().fa_fwd_order_len(ctypes.byref(fa))
-        assert n == len(lens_q) * ((mq + 127) // 128)
+        assert n == len(lens_q) * ((mq + 31) // 32)
         order = torch.full((n,), -7, dtype=torch.int32, device=device)
         if ordered:
             fa.work_order = order.data_ptr()
@@ -140,7 +149,10 @@ def test_fwd_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, h
         res[ordered] = (o.cpu(), lse.cpu())
         if ordered:
             cus = torch.cuda.get_device_properties(0).multi_processor_count
-            bm = 256 if hd == 128 and ((mq + 255) // 256) * len(lens_q) * h >= 2 * cus and mq >= 2048 else 128
+            # Positions per workgroup: 256 rows (ping-pong) or 128, over gp heads.
+            gp = _fwd_pack(h, hk, 256)
+            pp_grid = -(-mq * gp // 256) * len(lens_q) * (h // gp)
+            bm = 256 // gp if hd == 128 and pp_grid >= 2 * cus and mq >= 2048 else 128 // _fwd_pack(h, hk, 128)
             nmb = (mq + bm - 1) // bm
             got = order.cpu().tolist()[: len(lens_q) * nmb]
             assert sorted(got) == list(range(len(lens_q) * nmb)), "every item exactly once"

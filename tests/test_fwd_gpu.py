@@ -59,12 +59,13 @@ def test_fwd_parity(device, hd, causal, sq, sk, heads, batch, scale):
                                           (True, 2400, 2400)])
 def test_fwd_pingpong_shapes(device, causal, sq, sk):
     """Shapes on which fa_fwd takes the ping-pong kernel (head_dim 128, at least
-    2048 query rows and a grid of 256-row blocks at least twice the CU count):
-    non-causal, ragged ends, sq != sk both ways, GQA 16 / 4.  Batch row 0 of
-    every head against the oracle (the whole batch runs on the GPU)."""
+    2048 query rows and a grid of 256-row workgroups at least twice the CU
+    count; GQA 16 / 4 packs 4 heads x 64 positions per workgroup): non-causal,
+    ragged ends, sq != sk both ways.  Batch row 0 of every head against the
+    oracle (the whole batch runs on the GPU)."""
     b, h, hk, hd = 4, 16, 4, 128
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    assert sq >= 2048 and ((sq + 255) // 256) * b * h >= 2 * cus, "shape must select the ping-pong kernel"
+    assert sq >= 2048 and ((sq + 63) // 64) * b * (h // 4) >= 2 * cus, "shape must select the ping-pong kernel"
     g = torch.Generator().manual_seed(1500 + sq + sk + int(causal))
     q = randn16((b, sq, h, hd), g)
     k = randn16((b, sk, hk, hd), g)
