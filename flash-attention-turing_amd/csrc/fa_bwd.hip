@@ -63,11 +63,14 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const fa_bwd_args a
 }
 
 // ---------------------------------------------------------------------------
-// dQ kernel: 4 waves x 32 queries of one (batch, head); 64-key blocks of K and
-// V copied HBM -> LDS (two stages, global_load_lds); S^T = K Q^T and
-// dP^T = V dO^T read K, V as natural A operands, dQ^T += K^T dS^T reads K
-// transposed (ds_read_b64_tr_b16).  The prologue computes D = rowsum(dO * O)
-// for the workgroup's rows and stores -D for the dK/dV kernel.
+// dQ kernel: 4 waves x 32 queries; 64-key blocks of K and V copied HBM -> LDS
+// (two stages, global_load_lds); S^T = K Q^T and dP^T = V dO^T read K, V as
+// natural A operands, dQ^T += K^T dS^T reads K transposed
+// (ds_read_b64_tr_b16).  A workgroup holds gp = 2^lg query heads of one GQA
+// group (gp divides the group, so they share K / V) at P = 128 / gp positions
+// from m0: wave w takes head h + w / (P / 32), positions m0 + 32 (w % (P / 32))
+// onward, and the K / V tiles serve all gp heads.  The prologue computes
+// D = rowsum(dO * O) for the wave's rows and stores -D for the dK/dV kernel.
 template <int HD>
 struct DqCfg {
     static constexpr int BM = 128, BN = 64, NT = kBwdThreads;
@@ -76,7 +79,7 @@ struct DqCfg {
 };
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks) {
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks, const int lg) {
     using C = DqCfg<HD>;
     constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
@@ -84,29 +87,32 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int col = lane & 31, hh = lane >> 5;
+    const int packs = a.nheads >> lg;  // head packs per batch
     int b, h, mb;
     if (a.work_order && a.cu_seqlens_q) {
-        // Item of the device-built order (heads fastest); -1: no query rows.
+        // Item of the device-built order (head packs fastest); -1: no query rows.
         const int nnb = (a.seqlen_k + 127) / 128;
-        const int it = a.work_order[int64_t(a.batch) * nnb + blockIdx.x / a.nheads];
+        const int it = a.work_order[int64_t(a.batch) * nnb + blockIdx.x / packs];
         if (it < 0) return;
         b = __builtin_amdgcn_readfirstlane(it / num_m_blocks);
         mb = __builtin_amdgcn_readfirstlane(it - b * num_m_blocks);
-        h = blockIdx.x % a.nheads;
+        h = (blockIdx.x % packs) << lg;
     } else {
-        const int bh_count = a.batch * a.nheads;
-        const int bh = blockIdx.x % bh_count;
-        mb = blockIdx.x / bh_count;
+        const int bp_count = a.batch * packs;
+        const int bp = blockIdx.x % bp_count;
+        mb = blockIdx.x / bp_count;
         if (CAUSAL) mb = num_m_blocks - 1 - mb;
-        b = bh / a.nheads;
-        h = bh - b * a.nheads;
+        b = bp / packs;
+        h = (bp - b * packs) << lg;
     }
     const int hk = h / (a.nheads / a.nheads_k);
     const bool packed_q = a.cu_seqlens_q != nullptr, packed_k = a.cu_seqlens_k != nullptr;
     const SeqInfo si = seq_info(b, a.seqlen_q, a.seqlen_k, a.cu_seqlens_q, a.cu_seqlens_k, nullptr, 0);
     const int sq = si.sq, sk = si.sk;
-    const int m0 = mb * BM;
+    const int P = BM >> lg;  // positions per head
+    const int m0 = mb * P;
     if (m0 >= sq) return;
+    h += wave >> (2 - lg);  // this wave's head: P / 32 = 2^(2 - lg) waves per head
 
     const f16 *qp = (const f16 *)a.q.ptr + base_off(a.q, packed_q, b, si.q_start, h);
     const f16 *dop = (const f16 *)a.dout.ptr + base_off(a.dout, packed_q, b, si.q_start, h);
@@ -119,7 +125,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 
     const int causal_off = sk - sq;
     int n_end = sk;
-    if (CAUSAL) n_end = max(0, min(sk, m0 + BM + causal_off));
+    if (CAUSAL) n_end = max(0, min(sk, m0 + P + causal_off));
     const int n_blocks = (n_end + BN - 1) / BN;
     const float cs = a.softmax_scale * kLog2e;
 
@@ -144,7 +150,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 
     // Q^T, dO^T as B operands (lane: query col, d = 16g + 8hh + 0..7) and this
     // lane's half of D = sum_d O * dO.
-    const int qi = m0 + wave * 32 + col;
+    const int q_lo = m0 + 32 * (wave & ((P >> 5) - 1));
+    const int qi = q_lo + col;
     const bool qv = qi < sq;
     f16x8 qB[HD / 16], doB[HD / 16];
     float dpart = 0.f;
@@ -170,7 +177,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     TileReader<HD> rd;
     rd.init(lane);
 
-    const int q_lo = m0 + wave * 32;
     auto block = [&](int nb, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = nb & 1;
@@ -265,9 +271,9 @@ struct DkvCfg {
 // Varlen work orders (order_items in fa_common.h).  dK/dV: item it = b * nnb
 // + nb is key block nb of sequence b, its work the number of query rows that
 // see the block (causal: min(sq, sk - 128 nb), else sq), in 64-row buckets;
-// dQ: item it = b * nmb + mb is query block mb (128 rows), its work the keys
-// the block's last row sees (causal: min(sk, 128 (mb + 1) + sk - sq), else
-// sk), in 64-key buckets.  The list of the dK/dV items comes first in
+// dQ: item it = b * nmb + mb is block mb of P query positions, its work the
+// keys the block's last position sees (causal: min(sk, P (mb + 1) + sk - sq),
+// else sk), in 64-key buckets.  The list of the dK/dV items comes first in
 // work_order, that of the dQ items after it (fa_bwd_order_len).
 __global__ __launch_bounds__(kOrderThreads) void bwd_order_kernel(const fa_bwd_args a, const int nnb) {
     order_items(a.batch * nnb, [&](int it) {
@@ -281,14 +287,15 @@ __global__ __launch_bounds__(kOrderThreads) void bwd_order_kernel(const fa_bwd_a
     }, a.work_order, false);
 }
 
-__global__ __launch_bounds__(kOrderThreads) void dq_order_kernel(const fa_bwd_args a, const int nnb, const int nmb) {
+__global__ __launch_bounds__(kOrderThreads) void dq_order_kernel(const fa_bwd_args a, const int nnb, const int nmb,
+                                                                 const int P) {
     order_items(a.batch * nmb, [&](int it) {
         const int b = it / nmb, mb = it - b * nmb;
         const int sq = a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b];
         const int sk = a.cu_seqlens_k ? a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b] : a.seqlen_k;
-        const int m0 = mb * 128;
+        const int m0 = mb * P;
         if (m0 >= sq) return -1;
-        const int keys = a.causal ? max(0, min(sk, m0 + 128 + sk - sq)) : sk;
+        const int keys = a.causal ? max(0, min(sk, m0 + P + sk - sq)) : sk;
         return min(keys >> 6, kOrderBuckets - 1);
     }, a.work_order + int64_t(a.batch) * nnb, false);
 }
@@ -602,18 +609,24 @@ static int launch_preprocess(const fa_bwd_args &a, hipStream_t s) {
 
 template <int HD, bool CAUSAL>
 static int launch_dq(const fa_bwd_args &a, hipStream_t s) {
-    const int nmb = (a.lse_seqlen + DqCfg<HD>::BM - 1) / DqCfg<HD>::BM;
-    const int64_t grid = int64_t(nmb) * a.batch * a.nheads;
+    // Query heads per workgroup: the largest power of two dividing the GQA
+    // group, up to one per wave (they share the K / V tiles).
+    static_assert(DqCfg<HD>::BM == 128, "the dQ kernel packs at most 4 heads of 32 rows");
+    const int group = a.nheads / a.nheads_k;
+    int lg = 0;
+    while (lg < 2 && group % (2 << lg) == 0) ++lg;
+    const int P = DqCfg<HD>::BM >> lg;
+    const int nmb = (a.lse_seqlen + P - 1) / P;
+    const int64_t grid = int64_t(nmb) * a.batch * (a.nheads >> lg);
     if (grid == 0) return FA_OK;
     if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
-    static_assert(DqCfg<HD>::BM == 128, "dq_order_kernel and fa_bwd_order_len assume 128-query blocks");
     if (a.work_order && a.cu_seqlens_q) {
         const int nnb = (a.seqlen_k + 127) / 128;
-        hipLaunchKernelGGL(dq_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, a, nnb, nmb);
+        hipLaunchKernelGGL(dq_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, a, nnb, nmb, P);
         const int rc = int(hipGetLastError());
         if (rc) return rc;
     }
-    hipLaunchKernelGGL((bwd_dq_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a, nmb);
+    hipLaunchKernelGGL((bwd_dq_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(kBwdThreads), 0, s, a, nmb, lg);
     return int(hipGetLastError());
 }
 
@@ -676,7 +689,7 @@ extern "C" int fa_bwd_dkdv(const fa_bwd_args *args, void *stream) {
 extern "C" size_t fa_bwd_order_len(const fa_bwd_args *a) {
     if (!a || a->batch <= 0) return 0;
     const size_t nnb = size_t((std::max(a->seqlen_k, 0) + 127) / 128);
-    const size_t nmb = size_t((std::max(a->lse_seqlen, 0) + 127) / 128);
+    const size_t nmb = size_t((std::max(a->lse_seqlen, 0) + 31) / 32);  // dQ blocks of 32 positions at the least
     return size_t(a->batch) * (nnb + nmb);
 }
 

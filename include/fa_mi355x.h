@@ -111,7 +111,7 @@ typedef struct fa_bwd_args {
 } fa_bwd_args;
 
 /* Length in int32s of the work_order workspace: batch * (ceil(seqlen_k / 128) +
- * ceil(lse_seqlen / 128)).  No counterpart in the reference (its grids are in
+ * ceil(lse_seqlen / 32)).  No counterpart in the reference (its grids are in
  * natural order). */
 size_t fa_bwd_order_len(const fa_bwd_args *args);
 /* D = rowsum(dO * O) (flash_bwd_preprocess_kernel.h:23-96), stored negated in dsum plane 0. */

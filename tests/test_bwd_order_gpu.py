@@ -3,7 +3,7 @@ and dQ lists) and fa_fwd_args.
 
 With the workspace, fa_bwd lists the (sequence, key block) items on the device,
 most query rows first, and launches the dK/dV workgroups in that order (and the
-dQ kernel its (sequence, query block) items, most keys first).  Every
+dQ kernel its (sequence, block of query positions) items, most keys first).  Every
 item is computed independently, so dQ, dK and dV must be bit-identical to the
 natural-order launch; the list itself must hold every item with keys exactly
 once, in non-increasing 64-row buckets of the rows that see the key block
@@ -58,8 +58,10 @@ def test_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, hd, c
         dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=device)
         ba = fa_capi.bwd_args(q, k, v, o, lse, do, dq, dk, dv, dsum, s, causal, cq, ck, mq, mk)
         n = fa_capi.load().fa_bwd_order_len(ctypes.byref(ba))
-        nnb, nmb = (mk + 127) // 128, (mq + 127) // 128
-        assert n == len(lens_q) * (nnb + nmb)
+        # dQ blocks hold P = 128 / gp positions of gp heads of a GQA group.
+        nnb, p_dq = (mk + 127) // 128, 128 // _head_pack(h, hk, 128)
+        nmb = (mq + p_dq - 1) // p_dq
+        assert n == len(lens_q) * (nnb + (mq + 31) // 32)
         order = torch.full((n,), -7, dtype=torch.int32, device=device)
         if ordered:
             ba.work_order = order.data_ptr()
@@ -81,13 +83,13 @@ def test_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, hd, c
             buckets = [expect[i] for i in live]
             assert all(x >= y for x, y in zip(buckets, buckets[1:])), "items must come most rows first"
             # The dQ list (second part): query blocks by the keys their last row sees.
-            got_q = order.cpu().tolist()[len(lens_q) * nnb:]
+            got_q = order.cpu().tolist()[len(lens_q) * nnb: len(lens_q) * (nnb + nmb)]
             expect_q = {}
             for b in range(len(lens_q)):
                 for mb in range(nmb):
-                    m0 = 128 * mb
+                    m0 = p_dq * mb
                     if m0 < lens_q[b]:
-                        keys = max(0, min(lens_k[b], m0 + 128 + lens_k[b] - lens_q[b])) if causal else lens_k[b]
+                        keys = max(0, min(lens_k[b], m0 + p_dq + lens_k[b] - lens_q[b])) if causal else lens_k[b]
                         expect_q[b * nmb + mb] = min(keys // 64, 1023)
             live_q = got_q[: len(expect_q)]
             assert sorted(live_q) == sorted(expect_q) and all(x == -1 for x in got_q[len(expect_q):])
@@ -100,8 +102,8 @@ def test_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, hd, c
                  causal)
 
 
-def _fwd_pack(h, hk, bm):
-    """Query heads per forward workgroup: the largest power of two dividing
+def _head_pack(h, hk, bm):
+    """Query heads per forward or dQ workgroup: the largest power of two dividing
     the GQA group that leaves whole 32-row tiles per head."""
     gp = 1
     while 2 * gp <= bm // 32 and (h // hk) % (2 * gp) == 0:
@@ -150,9 +152,9 @@ def test_fwd_work_order_same_results_and_sorted(device, lens_q, lens_k, h, hk, h
         if ordered:
             cus = torch.cuda.get_device_properties(0).multi_processor_count
             # Positions per workgroup: 256 rows (ping-pong) or 128, over gp heads.
-            gp = _fwd_pack(h, hk, 256)
+            gp = _head_pack(h, hk, 256)
             pp_grid = -(-mq * gp // 256) * len(lens_q) * (h // gp)
-            bm = 256 // gp if hd == 128 and pp_grid >= 2 * cus and mq >= 2048 else 128 // _fwd_pack(h, hk, 128)
+            bm = 256 // gp if hd == 128 and pp_grid >= 2 * cus and mq >= 2048 else 128 // _head_pack(h, hk, 128)
             nmb = (mq + bm - 1) // bm
             got = order.cpu().tolist()[: len(lens_q) * nmb]
             assert sorted(got) == list(range(len(lens_q) * nmb)), "every item exactly once"
