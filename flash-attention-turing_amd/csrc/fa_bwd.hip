@@ -26,6 +26,8 @@
 namespace fa {
 
 constexpr int kBwdThreads = 256;
+// MFMA steps by which the dQ kernel's LDS operand reads run ahead.
+constexpr int kDqPipe = 4;
 
 // ---------------------------------------------------------------------------
 // Preprocess: dsum[b][h][i] = -sum_d fp32(O) * fp32(dO) (stored negated, the
@@ -188,17 +190,42 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         if (q_lo >= sq) return;                                      // no query row of the sequence
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
+        // Operand reads run kDqPipe - 1 MFMA steps ahead through a ring of
+        // registers, with a scheduling fence per step, so an MFMA does not
+        // wait for the LDS read issued just before it.  The per-read
+        // addresses are recomputed from an opaque copy of the lane's bases
+        // (hoisted, they would hold registers for the whole kernel).
+        TileReader<HD> r = rd;
+        asm volatile("" : "+v"(r.a_base), "+v"(r.tr_base[0]), "+v"(r.tr_base[1]));
+        f16x8 opnd[kDqPipe];
+        // S / dP step t: chain c = t % 4 (s[0], dp[0], s[1], dp[1]) at K step
+        // g = t / 4, so consecutive MFMAs feed four independent accumulators
+        // and each chain still sums g = 0, 1, ... in order.
+        constexpr int NSD = 4 * (HD / 16), NDQ = 4 * (HD / 32), NDT = HD / 32;
+        auto read_sd = [&](int t) FA_INLINE {
+            const int c = t & 3;
+            opnd[t % kDqPipe] = r.a_operand((c & 1) ? vs : ks, 32 * (c >> 1), t >> 2);
+        };
+        // dQ step u: accumulator dt = u % NDT at key step gg = u / NDT.
+        auto read_dq = [&](int u) FA_INLINE { opnd[u % kDqPipe] = r.tr_operand(ks, 16 * (u / NDT), u % NDT); };
         f32x16 s[2], dp[2];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = mfma32(rd.a_operand(ks, 32 * t, 0), qB[0], zero16());
-            dp[t] = mfma32(rd.a_operand(vs, 32 * t, 0), doB[0], zero16());
+        for (int t = 0; t < kDqPipe - 1; ++t) read_sd(t);
 #pragma unroll
-            for (int g = 1; g < HD / 16; ++g) {
-                s[t] = mfma32(rd.a_operand(ks, 32 * t, g), qB[g], s[t]);
-                dp[t] = mfma32(rd.a_operand(vs, 32 * t, g), doB[g], dp[t]);
-            }
+        for (int t = 0; t < NSD; ++t) {
+            if (t + kDqPipe - 1 < NSD) read_sd(t + kDqPipe - 1);
+            const int c = t & 3, g = t >> 2;
+            if (c & 1)
+                dp[c >> 1] = mfma32(opnd[t % kDqPipe], doB[g], g == 0 ? zero16() : dp[c >> 1]);
+            else
+                s[c >> 1] = mfma32(opnd[t % kDqPipe], qB[g], g == 0 ? zero16() : s[c >> 1]);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        // The first K^T reads of the dQ product do not depend on dS: they go
+        // out before the softmax, which hides their latency.
+#pragma unroll
+        for (int u = 0; u < kDqPipe - 1; ++u) read_dq(u);
         const int lim = (CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1) - n0;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -211,10 +238,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         f16x8 dsB[4];
 #pragma unroll
         for (int gg = 0; gg < 4; ++gg) dsB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) dq[dt] = mfma32(rd.tr_operand(ks, 16 * gg, dt), dsB[gg], dq[dt]);
+        for (int u = 0; u < NDQ; ++u) {
+            if (u + kDqPipe - 1 < NDQ) read_dq(u + kDqPipe - 1);
+            dq[u % NDT] = mfma32(opnd[u % kDqPipe], dsB[u / NDT], dq[u % NDT]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // Blocks [0, n_full) are fully visible to every row of the workgroup.

@@ -31,8 +31,6 @@
 
 #include "fa_common.h"
 
-#define FA_INLINE __attribute__((always_inline))
-
 namespace fa {
 
 constexpr int kFwdBN = 64;  // keys per block
