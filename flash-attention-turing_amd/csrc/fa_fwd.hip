@@ -25,8 +25,8 @@
 //     operand reads and MFMAs) and a softmax phase (block j's exponentials),
 //     separated by workgroup barriers, so one group's softmax runs on the
 //     VALU while the other group's MFMAs run on the matrix cores;
-//   * fwd_kernel (head_dim 64 and small grids): 4 waves, two independent
-//     workgroups per CU.
+//   * fwd_kernel (head_dim 64 and small grids): 4 waves, two (head_dim 128)
+//     or three (head_dim 64) independent workgroups per CU.
 #include <type_traits>
 
 #include "fa_common.h"
@@ -53,6 +53,7 @@ struct FwdCfg {
 // maximum, as it does with P = 1 in the reference.  The LSE uses the fp32 sum
 // of the unrounded P (l_p), as the reference does.
 constexpr float kRescaleSlack = 8.f;
+constexpr float kRescaleLimit = 256.f;  // 2^kRescaleSlack
 
 // Sum of the eight fp16 values of an MFMA operand, accumulated in fp32.
 __device__ __forceinline__ float sum8(const f16x8 &v, float acc) {
@@ -226,6 +227,39 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f3
     }
 }
 
+// The same block without the row maximum, for kernels that can recompute S:
+// P = exp2(S*c - m) against the current maximum stands when every row of the
+// wave already has one and no P exceeds 2^kRescaleSlack (the row's sum of P
+// bounds each of them).  softmax_block would then not raise the maximum
+// either, so the results are the same bits; otherwise (a row's first visible
+// keys, or a score that outgrows the maximum) S is left overwritten and the
+// caller recomputes it and runs softmax_block.  Returns true on success
+// (wave-uniform).
+template <int HD, bool MASK>
+__device__ __forceinline__ bool softmax_block_fast(f32x16 (&s)[2], f16x8 (&pB)[4], SoftmaxRow &r, float cscale,
+                                                   int lim, int hh) {
+    const bool have = r.m_t != -INFINITY;
+    const float m_use = have ? r.m_t : 0.f;
+    float rs = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float p = exp2_fast(fmaf(s[kt][e], cscale, -m_use));
+            if constexpr (MASK) p = kt * 32 + acc_lrow(e, hh) > lim ? 0.f : p;
+            s[kt][e] = p;
+            rs += p;
+        }
+    if (__builtin_amdgcn_ballot_w64(!(have && rs <= kRescaleLimit)) != 0) return false;
+    r.l_p += rs;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+        pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
+        r.l_o = sum8(pB[gg], r.l_o);
+    }
+    return true;
+}
+
 // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
 template <int HD>
 __device__ __forceinline__ void store_row(const fa_fwd_args &a, const FwdWork &w, int qi, int hh,
@@ -279,10 +313,13 @@ struct KvLoader {
 
 // ---------------------------------------------------------------------------
 // 4-wave kernel: each wave runs S, softmax and PV of a block in turn; two
-// workgroups per CU (64 KB LDS each at head_dim 128) overlap one wave's
-// softmax with the other's MFMAs on each SIMD.
+// workgroups per CU at head_dim 128 (64 KB LDS, 246 registers), three at
+// head_dim 64 (32 KB LDS, at most 168 registers), overlap one wave's softmax
+// with the others' MFMAs on each SIMD.  At head_dim 64 the kernel is bound by
+// VALU work, so its blocks first try the softmax without the row maximum
+// (softmax_block_fast).
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks, const int lg) {
+__global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks, const int lg) {
     constexpr int NT = 256;
     using C = FwdCfg<HD, NT>;
     constexpr int BM = C::BM, BN = C::BN;
@@ -329,15 +366,28 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const fa_fwd_args a, const 
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
         f32x16 s[2];
+        auto scores = [&]() FA_INLINE {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
+            for (int kt = 0; kt < 2; ++kt) {
+                s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
 #pragma unroll
-            for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
-        }
+                for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
+            }
+        };
+        scores();
         const int lim = (CAUSAL ? min(w.sk - 1, qi + w.causal_off) : w.sk - 1) - n0;
         f16x8 pB[4];
-        softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
+        // K_nb stays in this stage until the next block's barrier, so S can be
+        // recomputed when the maximum-free softmax does not stand.  Head_dim 64
+        // only: at 128 the second S product pushes the kernel into spills.
+        if constexpr (HD == 64) {
+            if (!softmax_block_fast<HD, MASK>(s, pB, row, w.cscale, lim, hh)) {
+                scores();
+                softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
+            }
+        } else {
+            softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
+        }
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll

@@ -156,3 +156,34 @@ def test_fwd_and_bwd_misaligned_base(device):
     grads_a = fai._flash_attn_backward(doa, qa, ka, va, out_a, lse_a, 0.125, True)
     for x, y in zip(grads, grads_a):
         assert torch.equal(x, y)
+
+
+# Key blocks whose scores jump far above every earlier block (keys scaled up
+# block by block), so a row's running maximum must rise by more than the
+# kernels' rescale slack several times, and exponentials taken against the
+# stale maximum overflow fp32: at head_dim 64 these blocks leave the
+# maximum-free softmax for the recomputed-S path.  sq > sk causal adds rows
+# with no visible key (their maximum never leaves -inf).
+@pytest.mark.gpu
+@pytest.mark.parametrize("hd,causal,sq,sk", [(64, False, 200, 640), (64, True, 640, 640), (64, True, 700, 300),
+                                             (128, False, 200, 640), (128, True, 700, 300)])
+def test_fwd_rising_maximum(device, hd, causal, sq, sk):
+    h, hk = 4, 2
+    g = torch.Generator().manual_seed(1700 + hd + sq + sk + int(causal))
+    q = randn16((1, sq, h, hd), g)
+    k = randn16((1, sk, hk, hd), g).float()
+    v = randn16((1, sk, hk, hd), g)
+    gain = torch.ones(sk)
+    gain[64:] = 4.0
+    gain[192:] = 16.0
+    gain[448:] = 40.0
+    k = (k * gain[None, :, None, None]).to(torch.float16)
+    s = hd ** -0.5
+    print(f"case rising maximum hd={hd} causal={causal} sq={sq} sk={sk}", flush=True)
+    out, lse = fai._flash_attn_forward(q.to(device), k.to(device), v.to(device), s, causal)
+    torch.cuda.synchronize()
+    o_ref, l_ref = attention_fwd(q, k, v, s, causal)
+    o_twin, _ = fwd_twin(q, k, v, s, causal)
+    assert torch.isfinite(out).all()
+    assert_2x("out", out, o_ref, o_twin)
+    assert_lse(lse, l_ref)
