@@ -175,6 +175,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     f32x16 dq[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) dq[i] = zero16();
+    // At head_dim 64 (bound by VALU work) the dP^T accumulators start from -D,
+    // so dP - D comes out of the MFMAs; at 128 the 16 registers of that seed
+    // do not fit and D is subtracted per element.
+    f32x16 dp_init = zero16();
+    if constexpr (HD == 64) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dp_init[i] = -dsum;
+    }
 
     TileReader<HD> rd;
     rd.init(lane);
@@ -217,7 +225,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
             if (t + kDqPipe - 1 < NSD) read_sd(t + kDqPipe - 1);
             const int c = t & 3, g = t >> 2;
             if (c & 1)
-                dp[c >> 1] = mfma32(opnd[t % kDqPipe], doB[g], g == 0 ? zero16() : dp[c >> 1]);
+                dp[c >> 1] = mfma32(opnd[t % kDqPipe], doB[g], g == 0 ? dp_init : dp[c >> 1]);
             else
                 s[c >> 1] = mfma32(opnd[t % kDqPipe], qB[g], g == 0 ? zero16() : s[c >> 1]);
             __builtin_amdgcn_sched_barrier(0);
@@ -233,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
             for (int r = 0; r < 16; ++r) {
                 float p = exp2_fast(fmaf(s[t][r], cs, -lse2));
                 if constexpr (MASK) p = t * 32 + acc_lrow(r, hh) > lim ? 0.f : p;
-                s[t][r] = p * (dp[t][r] - dsum);
+                s[t][r] = HD == 64 ? p * dp[t][r] : p * (dp[t][r] - dsum);
             }
         f16x8 dsB[4];
 #pragma unroll
