@@ -231,9 +231,11 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f3
 // P = exp2(S*c - m) against the current maximum stands when every row of the
 // wave already has one and no P exceeds 2^kRescaleSlack (the row's sum of P
 // bounds each of them).  softmax_block would then not raise the maximum
-// either, so the results are the same bits; otherwise (a row's first visible
-// keys, or a score that outgrows the maximum) S is left overwritten and the
-// caller recomputes it and runs softmax_block.  Returns true on success
+// either, so the results are the same bits (but for a score within fp32
+// rounding of the slack bound, where the two tests can decide differently and
+// both results are exact to rounding); otherwise (a row's first visible keys,
+// or a score that outgrows the maximum) S is left overwritten and the caller
+// recomputes it and runs softmax_block.  Returns true on success
 // (wave-uniform).
 template <int HD, bool MASK>
 __device__ __forceinline__ bool softmax_block_fast(f32x16 (&s)[2], f16x8 (&pB)[4], SoftmaxRow &r, float cscale,
