@@ -174,6 +174,9 @@ def c3_checked_sequences(lens):
 FULLSIZE = {
     "c2": (4, 4096, 16, 128, 12, True, ((0, 0, 16), (3, 0, 16))),
     "s8192": (4, 8192, 16, 128, 17, True, ((0, 0, 8), (0, 8, 16), (3, 0, 8), (3, 8, 16))),
+    # benchmark.sh's head_dim 64 point at the north-star length (its forward and dQ kernels
+    # have their own head_dim 64 forms); one 8-head half of rows 0 and 3.
+    "hd64_s8192": (4, 8192, 16, 64, 19, True, ((0, 0, 8), (3, 8, 16))),
 }
 
 

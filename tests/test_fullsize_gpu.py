@@ -6,7 +6,8 @@ rounding-point twin are evaluated on the CPU for the parts that finish in
 seconds there:
 
 * c1 (b2 s512 h8 d64, non-causal forward): every element;
-* c2 (b4 s4096 h16 d128 causal, forward + backward) and the s8192 point:
+* c2 (b4 s4096 h16 d128 causal, forward + backward), the s8192 point and its
+  head_dim 64 counterpart (b4 s8192 h16 d64 causal, one 8-head half of rows 0 and 3):
   every element of batch rows 0 and 3 (rows of a batch are independent, so
   each is the full computation of that row at the full sequence length and
   head count), checked four KV heads at a time (the s8192 rows as two tests
@@ -121,6 +122,14 @@ def test_c2_full_forward_backward(device, unit):
 def test_s8192_north_star_forward_backward(device, unit):
     """The shape the north star's MFMA targets are quoted on (benchmark.sh:17-21)."""
     _check_dense_unit(device, "s8192", unit)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("unit", FULLSIZE["hd64_s8192"][6])
+def test_hd64_s8192_forward_backward(device, unit):
+    """benchmark.sh's head_dim 64 shape at seqlen 8192, causal (benchmark.sh:17-23): the
+    head_dim 64 forms of the forward (softmax without the row maximum) and dQ (dP from -D)."""
+    _check_dense_unit(device, "hd64_s8192", unit)
 
 
 @pytest.mark.gpu
