@@ -18,8 +18,8 @@ inputs already resident in HBM:
   (``decode_c4_window4k``: an upstream option the reference rejects).
   ``--no-8k`` keeps only the headline shapes (c2, c4).
 * the reference's own published metric (README.md:24-48): at benchmark.sh's
-  shapes (batch 4, 16 heads, head_dim 64 / 128, causal or not; seqlen 4096
-  and 8192 here) the forward and backward kernel time of PyTorch's
+  shapes (batch 4, 16 heads, head_dim 64 / 128, causal or not; seqlen 4096,
+  8192, 16000 and 16384 here) the forward and backward kernel time of PyTorch's
   scaled_dot_product_attention on the same GPU over this build's
   (``vs_torch_sdpa_gpu``: speedups > 1 mean this build is faster).
 
@@ -494,15 +494,20 @@ def cpu_baseline_decode(device, n_seq=8):
     }
 
 
+# The sweep's sequence lengths: benchmark.sh:21 runs 512-16384 and the odd lengths
+# 500-16000; its README quotes the speedups (README.md:30) at the long end.
+SWEEP_SEQLENS = (4096, 8192, 16000, 16384)
+
+
 def sweep_legs(device, steps, warmup):
     """benchmark.sh:17-38's shapes (batch 4, 16 heads): head_dim 64 / 128, causal or not,
-    seqlen 4096 and 8192; forward and backward TFLOPS per shape."""
+    seqlen 4096, 8192, 16000 and 16384; forward and backward TFLOPS per shape."""
     import torch
 
     out = {}
     for hd in (64, 128):
         for causal in (False, True):
-            for s in (4096, 8192):
+            for s in SWEEP_SEQLENS:
                 launches, tensors = train_step_setup(4, s, 16, hd, 7, device, causal)
                 ms, per = Timed(launches).run(steps, warmup)
                 rep, _, _ = train_report(4, s, 16, hd, ms, per, causal)
@@ -640,7 +645,7 @@ def main():
             torch.cuda.empty_cache()
 
     if args.only in ("all", "train") and not args.no_8k:
-        log("sweep: b4 h16, head_dim 64/128, causal and not, seqlen 4096/8192 (seed 7)")
+        log("sweep: b4 h16, head_dim 64/128, causal and not, seqlen 4096/8192/16000/16384 (seed 7)")
         result["sweep_b4_h16"] = sweep_legs(device, max(3, args.steps // 4), max(1, args.warmup // 4))
         log(f"sweep: {result['sweep_b4_h16']}")
         log("torch SDPA on this GPU at the sweep's shapes (the reference's published speedup metric)")

@@ -1,7 +1,7 @@
 // Shared C-ABI utilities: argument checks and error strings.
 #include <hip/hip_runtime.h>
 
-#include "fa_mi355x.h"
+#include "fa_common.h"
 
 namespace fa {
 // Compute units of the current device, queried once per device (launch shapes).
@@ -16,14 +16,14 @@ int device_cus() {
     }
     return cached[dev];
 }
-}  // namespace fa
 
-extern "C" int fa_check_tensor(const fa_tensor &t, bool required) {
+int check_tensor(const fa_tensor &t, bool required) {
     if (!t.ptr) return required ? FA_ERR_INVALID_ARG : FA_OK;
     if ((reinterpret_cast<uintptr_t>(t.ptr) & 15u) != 0) return FA_ERR_INVALID_ARG;
     if ((t.batch_stride & 7) || (t.row_stride & 7) || (t.head_stride & 7)) return FA_ERR_INVALID_ARG;
     return FA_OK;
 }
+}  // namespace fa
 
 extern "C" const char *fa_error_string(int code) {
     switch (code) {
@@ -42,3 +42,5 @@ extern "C" const char *fa_error_string(int code) {
             return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "fa_mi355x: unknown error";
     }
 }
+
+extern "C" int fa_abi_version(void) { return FA_ABI_VERSION; }

@@ -687,12 +687,10 @@ static int launch_dkdv(const fa_bwd_args &a, hipStream_t s) {
 
 }  // namespace fa
 
-extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
-
 static int check_bwd_tensors(const fa_bwd_args *a) {
     const fa_tensor *ts[] = {&a->q, &a->k, &a->v, &a->o, &a->dout, &a->dq, &a->dk, &a->dv};
     for (const fa_tensor *t : ts)
-        if (fa_check_tensor(*t, true)) return FA_ERR_INVALID_ARG;
+        if (fa::check_tensor(*t, true)) return FA_ERR_INVALID_ARG;
     return FA_OK;
 }
 

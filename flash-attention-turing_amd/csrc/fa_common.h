@@ -26,6 +26,10 @@ namespace fa {
 
 // Compute units of the current device (host; fa_abi.hip).
 int device_cus();
+// FA_OK when t is usable by the kernels: a 16-byte aligned base and strides that
+// keep every row and head 16-byte aligned; a null pointer is an error only when
+// required (host; fa_abi.hip).
+int check_tensor(const fa_tensor &t, bool required);
 
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));

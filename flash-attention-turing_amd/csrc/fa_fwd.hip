@@ -647,8 +647,6 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
 
 }  // namespace fa
 
-extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
-
 extern "C" int fa_fwd(const fa_fwd_args *args, void *stream) {
     if (!args) return FA_ERR_INVALID_ARG;
     const fa_fwd_args &a = *args;
@@ -656,8 +654,8 @@ extern "C" int fa_fwd(const fa_fwd_args *args, void *stream) {
     if (a.batch < 0 || a.seqlen_q < 0 || a.seqlen_k < 0 || a.nheads <= 0 || a.nheads_k <= 0 ||
         a.nheads % a.nheads_k != 0 || !a.lse || a.lse_seqlen < a.seqlen_q)
         return FA_ERR_INVALID_ARG;
-    if (fa_check_tensor(a.q, true) || fa_check_tensor(a.k, true) || fa_check_tensor(a.v, true) ||
-        fa_check_tensor(a.o, true))
+    if (fa::check_tensor(a.q, true) || fa::check_tensor(a.k, true) || fa::check_tensor(a.v, true) ||
+        fa::check_tensor(a.o, true))
         return FA_ERR_INVALID_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (a.head_dim == 128)

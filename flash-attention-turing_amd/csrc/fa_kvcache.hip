@@ -39,6 +39,13 @@
 
 #include "fa_common.h"
 
+// The split kernel's fused combine publishes partials with relaxed agent-scope
+// atomics and relies on gfx950's write-through of agent-scope stores (see
+// kv_splitkv_kernel); this file is built for gfx950 only.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "fa_kvcache.hip targets gfx950: its fused combine relies on gfx950's agent-scope store visibility"
+#endif
+
 namespace fa {
 
 constexpr int kKvThreads = 256;
@@ -658,6 +665,11 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
             // the count to S has seen all S items' stores complete and reads the
             // partials with device-scope loads.  No cache-wide write-back or
             // invalidate is needed (both would stall this XCD's L2 once per item).
+            // This rests on gfx950's agent-scope accesses, not on the HIP memory
+            // model (the atomics are relaxed): an agent-scope store is written
+            // past the XCD's L2 before its vmcnt completes, and an agent-scope
+            // load does not hit another XCD's stale L2 copy; the #error at the
+            // top of this file keeps other targets from building it.
             wait_vmem();
             __syncthreads();
             if (tid == 0)
@@ -708,8 +720,6 @@ static int check_kv(const fa_kvcache_args *p) {
 
 }  // namespace fa
 
-extern "C" int fa_check_tensor(const fa_tensor &t, bool required);
-
 extern "C" int fa_kv_num_splits(int requested, int seqlen_k_capacity, int head_dim, int seqlen_q, int batch,
                                 int nheads, int nheads_k, int num_cus) {
     // An explicit request is honoured (kvcache_native.cu:922-924).  Otherwise
@@ -755,8 +765,8 @@ bool has_append(const fa_kvcache_args &a) { return a.k_new.ptr && a.seqlen_new >
 
 int check_append(const fa_kvcache_args &a) {
     if (!has_append(a)) return FA_OK;
-    if (!a.v_new.ptr || fa_check_tensor(a.k_new, true) || fa_check_tensor(a.v_new, true) ||
-        fa_check_tensor(a.k_cache, true) || fa_check_tensor(a.v_cache, true))
+    if (!a.v_new.ptr || fa::check_tensor(a.k_new, true) || fa::check_tensor(a.v_new, true) ||
+        fa::check_tensor(a.k_cache, true) || fa::check_tensor(a.v_cache, true))
         return FA_ERR_INVALID_ARG;
     return FA_OK;
 }
@@ -768,10 +778,12 @@ int64_t split_items(const fa_kvcache_args &a) {
 }
 
 int check_split(const fa_kvcache_args &a) {
-    if (fa_check_tensor(a.q, true) || fa_check_tensor(a.o, true) || fa_check_tensor(a.k_cache, true) ||
-        fa_check_tensor(a.v_cache, true))
+    if (fa::check_tensor(a.q, true) || fa::check_tensor(a.o, true) || fa::check_tensor(a.k_cache, true) ||
+        fa::check_tensor(a.v_cache, true))
         return FA_ERR_INVALID_ARG;
     if (a.num_splits > 1 && (!a.out_accum || !a.lse_accum)) return FA_ERR_WORKSPACE;
+    // The combine reads head_dim 128 partials as 64-bit (atomic) loads.
+    if (a.num_splits > 1 && (reinterpret_cast<uintptr_t>(a.out_accum) & 7u)) return FA_ERR_INVALID_ARG;
     if (split_items(a) > 0x7fffffff) return FA_ERR_INVALID_ARG;
     return FA_OK;
 }
@@ -912,9 +924,18 @@ int scratch_address(void **out) {
     if (dev < 0 || dev >= kMaxDevices) return FA_ERR_INVALID_ARG;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch[dev]) {
+        // The first call on a device may come from inside a stream capture whose
+        // mode forbids runtime calls that are not stream work (the lookup can
+        // load the code object on the device): relax this thread's mode for the
+        // lookup only; it enqueues nothing.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return int(e);
         void *p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess) return int(e);
+        if (e2 != hipSuccess) return int(e2);
         if (!p) return FA_ERR_SCRATCH;
         g_scratch[dev] = p;
     }

@@ -598,6 +598,9 @@ std::vector<at::Tensor> mha_fwd_kvcache(at::Tensor q, at::Tensor k_cache, at::Te
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    // The library found at load time must have the struct layouts this module was compiled with.
+    TORCH_CHECK(fa_abi_version() == FA_ABI_VERSION, "libfa_mi355x.so has argument-struct layout version ",
+                fa_abi_version(), ", flash_attn_turing was built against version ", FA_ABI_VERSION, ": rebuild both");
     m.def("fwd", &mha_fwd, "Forward pass");
     // dq / dk / dv (optional, after the reference's arguments): tensors the
     // gradients are written into, such as the slices of a packed dqkv.

@@ -88,6 +88,9 @@ _ARGP = {
     "fa_fwd_kvcache_noalloc": FaKvcacheArgs,
 }
 
+# FA_ABI_VERSION of include/fa_mi355x.h whose struct layouts the classes above mirror.
+ABI_VERSION = 3
+
 _lib = None
 
 
@@ -99,6 +102,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise ImportError(f"{path} is not built; run flash-attention-turing_amd/build.py")
     lib = ctypes.CDLL(path)
+    lib.fa_abi_version.restype = ctypes.c_int
+    if lib.fa_abi_version() != ABI_VERSION:
+        raise ImportError(f"{path} has argument-struct layout version {lib.fa_abi_version()}, this binding "
+                          f"declares version {ABI_VERSION}: rebuild the library or update fa_capi.py")
     for name, st in _ARGP.items():
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.POINTER(st), _p]

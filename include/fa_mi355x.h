@@ -237,6 +237,18 @@ int fa_fwd_kvcache_noalloc(const fa_kvcache_args *args, void *stream);
 /* Human-readable text for a return code (FA_* or hipError_t). */
 const char *fa_error_string(int code);
 
+/*
+ * Version of the argument-struct layouts above.  It changes whenever a struct
+ * gains, loses or moves a field (3: fa_fwd_args.work_order, fa_bwd_args.work_order
+ * and fa_kvcache_args.split_count appended).  A caller compiled against this
+ * header checks fa_abi_version() == FA_ABI_VERSION once after loading the
+ * library and refuses a mismatch: the entry points themselves cannot tell a
+ * shorter struct from an older caller.  No counterpart in the reference (its
+ * bindings are compiled together with its kernels).
+ */
+#define FA_ABI_VERSION 3
+int fa_abi_version(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,8 @@ for p in (REPO, TESTS):
 
 import torch  # noqa: E402
 
-from helpers import FULLSIZE, c3_checked_sequences, c3_inputs, dense_inputs, max_abs, unit_key  # noqa: E402
+from helpers import (FULLSIZE, FULLSIZE_KV_CHUNK, c1_inputs, c3_checked_sequences, c3_inputs, dense_inputs,  # noqa: E402
+                     max_abs, unit_key)
 from oracle.attention import attention_bwd, attention_fwd, bwd_fp32_noise  # noqa: E402
 from oracle.twin import bwd_twin, fwd_twin  # noqa: E402
 
@@ -85,7 +86,7 @@ def main():
         if want(key):
             record(key, *small_case(key))
     if want("c1"):
-        q, k, v = dense_inputs(2, 512, 8, 64, 11, n=3)
+        q, k, v = c1_inputs()
         record("c1", *twin_errors(q, k, v, None, 64 ** -0.5, False))
     for name, (b, s, h, d, seed, causal, units) in FULLSIZE.items():
         if not any(want(unit_key(name, u)) for u in units):
@@ -97,7 +98,7 @@ def main():
                 t = time.time()
                 r, hs = slice(u[0], u[0] + 1), slice(u[1], u[2])
                 record(key, *twin_errors(q[r, :, hs], k[r, :, hs], v[r, :, hs], do[r, :, hs], d ** -0.5, causal,
-                                         kv_chunk=4))
+                                         kv_chunk=FULLSIZE_KV_CHUNK.get(name, 4)))
                 print(f"  {time.time() - t:.0f} s", flush=True)
     if any(want(f"c3_seq{i}") for i in range(16)):
         lens, cu, q, k, v, do = c3_inputs()

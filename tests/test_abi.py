@@ -39,6 +39,15 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), f"{name} declared in fa_mi355x.h but not exported"
 
 
+def test_abi_version_matches_the_header(lib):
+    want = int(re.search(r"#define FA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    lib.fa_abi_version.restype = ctypes.c_int
+    assert lib.fa_abi_version() == want
+    import fa_capi
+
+    assert fa_capi.ABI_VERSION == want, "fa_capi.py's struct mirrors are for another layout version"
+
+
 def test_argument_errors_are_codes(lib):
     lib.fa_error_string.restype = ctypes.c_char_p
     assert lib.fa_fwd(None, None) == -1
@@ -185,6 +194,9 @@ def test_validation_errors_before_any_launch(lib):
     split = lib.fa_kv_splitkv
     split.argtypes = [ctypes.POINTER(fa_capi.FaKvcacheArgs), ctypes.c_void_p]
     assert split(ctypes.byref(kv), None) == -3
+    kv.out_accum, kv.lse_accum = P + 4, P  # 4-byte aligned accumulators: the combine reads 64-bit words
+    assert split(ctypes.byref(kv), None) == -1
+    kv.out_accum = kv.lse_accum = None
     kv.num_splits = 0
     assert split(ctypes.byref(kv), None) == -1  # num_splits must be >= 1 here
     kv.num_splits, kv.block_table, kv.page_block_size = 1, P, 100

@@ -11,13 +11,18 @@ seconds there:
   every element of batch rows 0 and 3 (rows of a batch are independent, so
   each is the full computation of that row at the full sequence length and
   head count), checked four KV heads at a time (the s8192 rows as two tests
-  of eight heads each);
+  of eight heads each); the reference's longest published length (b4 s16000
+  h16 d128 causal): two heads of rows 0 and 3;
 * c3 (16 packed causal sequences, 32/8 heads): every element of the shortest,
   the median-length and the longest sequence;
 * c4 (paged decode with append, 64 sequences up to 32k keys, 8 splits) and c5
   (4 remapped rows of an 8 x 131072 contiguous cache, 4 new tokens, 16 splits):
   every output and LSE, the appended K/V bit-exact, and every other cache
   position unchanged.
+
+The inputs are the ones bench.py times: the same seeds and draw order (c2 seed 1,
+s8192 seed 5, the sweep's shapes seed 7, c3 seed 2, c4 seed 3, c5 seed 4; c1,
+which bench.py does not time, seed 0).
 
 Bounds as in the small-size tests: 2x the twin's error (+ the fp32 noise
 floor for the backward), LSE to 2e-5 relative, bit-exact cache writes.  The
@@ -36,8 +41,8 @@ import pytest
 import torch
 
 import flash_attention_interface as fai
-from helpers import (FULLSIZE, assert_2x, assert_lse, c3_checked_sequences, c3_inputs, check_fwd_bwd, dense_inputs, randn16,
-                     unit_key)
+from helpers import (FULLSIZE, FULLSIZE_KV_CHUNK, assert_2x, assert_lse, c1_inputs, c3_checked_sequences, c3_inputs,
+                     check_fwd_bwd, dense_inputs, randn16, unit_key)
 from oracle import kvcache as okv
 
 REF_ERROR = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_error.json")))
@@ -69,7 +74,7 @@ def _check_against_fixture(key, stats):
 
 @pytest.mark.gpu
 def test_c1_full_forward(device):
-    q, k, v = dense_inputs(2, 512, 8, 64, 11, n=3)
+    q, k, v = c1_inputs()
     _log("c1: b2 s512 h8 d64 non-causal")
     out, lse = fai._flash_attn_forward(q.to(device), k.to(device), v.to(device), 64 ** -0.5, False)
     torch.cuda.synchronize()
@@ -106,7 +111,8 @@ def _check_dense_unit(device, name, unit):
     key = unit_key(name, unit)
     t = time.time()
     stats = check_fwd_bwd(key, q[r, :, hs], k[r, :, hs], v[r, :, hs], do[r, :, hs], out[r, :, hs], lse[r, hs],
-                          (dq[r, :, hs], dk[r, :, hs], dv[r, :, hs]), d ** -0.5, causal, kv_chunk=4, log=_log)
+                          (dq[r, :, hs], dk[r, :, hs], dv[r, :, hs]), d ** -0.5, causal,
+                          kv_chunk=FULLSIZE_KV_CHUNK.get(name, 4), log=_log)
     _log(f"{key}: forward and backward checked in {time.time() - t:.1f} s")
     _check_against_fixture(key, stats)
 
@@ -130,6 +136,14 @@ def test_hd64_s8192_forward_backward(device, unit):
     """benchmark.sh's head_dim 64 shape at seqlen 8192, causal (benchmark.sh:17-23): the
     head_dim 64 forms of the forward (softmax without the row maximum) and dQ (dP from -D)."""
     _check_dense_unit(device, "hd64_s8192", unit)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("unit", FULLSIZE["s16000"][6])
+def test_s16000_forward_backward(device, unit):
+    """The reference's longest published point (benchmark.sh:21; README.md:30 quotes its speedups at
+    s = 16000 / 16384): b4 s16000 h16 d128 causal, the sweep's seed; two heads of rows 0 and 3."""
+    _check_dense_unit(device, "s16000", unit)
 
 
 @pytest.mark.gpu
@@ -198,9 +212,10 @@ def _check_kvcache(tag, device, q, k_cache, v_cache, k_new, v_new, seqlens, batc
 
 @pytest.mark.gpu
 def test_c4_full_paged_decode(device):
+    """Config c4 drawn exactly as bench.py draws it (seed 3; the cache on the device generator)."""
     b, h, hk, d, page, splits = 64, 32, 8, 128, 256, 8
-    g = torch.Generator().manual_seed(15)
-    lens = torch.randint(1024, 32769, (b,), generator=g, dtype=torch.int32)
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, 32769, (b,), generator=g)
     nblk = [(int(x) + 1 + page - 1) // page for x in lens]
     perm = torch.randperm(sum(nblk), generator=g)
     table = torch.zeros((b, max(nblk)), dtype=torch.int32)
@@ -208,27 +223,28 @@ def test_c4_full_paged_decode(device):
     for i, n in enumerate(nblk):
         table[i, :n] = perm[off : off + n].to(torch.int32)
         off += n
+    gd = torch.Generator(device=device).manual_seed(3)
+    k_cache = torch.randn((sum(nblk), page, hk, d), generator=gd, device=device, dtype=torch.float16)
+    v_cache = torch.randn((sum(nblk), page, hk, d), generator=gd, device=device, dtype=torch.float16)
     q = randn16((b, 1, h, d), g)
     k_new = randn16((b, 1, hk, d), g)
     v_new = randn16((b, 1, hk, d), g)
-    gd = torch.Generator(device=device).manual_seed(15)
-    k_cache = torch.randn((sum(nblk), page, hk, d), generator=gd, device=device, dtype=torch.float16)
-    v_cache = torch.randn((sum(nblk), page, hk, d), generator=gd, device=device, dtype=torch.float16)
     _log(f"c4: paged decode, 64 sequences, {int(lens.sum()) + b} keys, {sum(nblk)} pages of 256")
-    _check_kvcache("c4", device, q, k_cache, v_cache, k_new, v_new, lens, None, table, splits)
+    _check_kvcache("c4", device, q, k_cache, v_cache, k_new, v_new, lens.to(torch.int32), None, table, splits)
 
 
 @pytest.mark.gpu
 def test_c5_full_long_context(device):
+    """Config c5 drawn exactly as bench.py draws it (seed 4; the cache on the device generator)."""
     rows, cap, h, d, b, sq, splits = 8, 131072, 16, 64, 4, 4, 16
-    g = torch.Generator().manual_seed(16)
+    g = torch.Generator().manual_seed(4)
     batch_idx = torch.randperm(rows, generator=g)[:b].to(torch.int32)
-    lens = torch.randint(65536, 131069, (b,), generator=g, dtype=torch.int32)
+    lens = torch.randint(65536, 131069, (b,), generator=g)
+    gd = torch.Generator(device=device).manual_seed(4)
+    k_cache = torch.randn((rows, cap, h, d), generator=gd, device=device, dtype=torch.float16)
+    v_cache = torch.randn((rows, cap, h, d), generator=gd, device=device, dtype=torch.float16)
     q = randn16((b, sq, h, d), g)
     k_new = randn16((b, sq, h, d), g)
     v_new = randn16((b, sq, h, d), g)
-    gd = torch.Generator(device=device).manual_seed(16)
-    k_cache = torch.randn((rows, cap, h, d), generator=gd, device=device, dtype=torch.float16)
-    v_cache = torch.randn((rows, cap, h, d), generator=gd, device=device, dtype=torch.float16)
     _log(f"c5: contiguous 8 x 131072 cache, rows {batch_idx.tolist()}, lengths {lens.tolist()}")
-    _check_kvcache("c5", device, q, k_cache, v_cache, k_new, v_new, lens, batch_idx, None, splits)
+    _check_kvcache("c5", device, q, k_cache, v_cache, k_new, v_new, lens.to(torch.int32), batch_idx, None, splits)

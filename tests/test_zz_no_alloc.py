@@ -1,9 +1,12 @@
 """fa_fwd_kvcache_noalloc (the allocation-free decode entry point) through the
-C ABI (collected last: it must pass alone and after every other test): same outputs, LSE and appended cache, bit for bit, as fa_fwd_kvcache
-with a caller workspace, on two calls in a row (the second smaller, so it
-runs over the first call's leftover scratch contents), with one split (no
-accumulators) and with splits; a request beyond the static scratch returns
-FA_ERR_SCRATCH without launching anything."""
+C ABI (collected last: it must pass alone and after every other test): same
+outputs, LSE and appended cache, bit for bit, as fa_fwd_kvcache with a caller
+workspace, on two calls in a row (the second smaller, so it runs over the
+first call's leftover scratch contents), with one split (no accumulators) and
+with splits; the process's first call made inside a HIP graph capture (the
+device's scratch address is looked up then) and the graph replayed with new
+cache lengths; a request beyond the static scratch returns FA_ERR_SCRATCH
+without launching anything."""
 
 import ctypes
 
@@ -55,9 +58,47 @@ def _call(device, name, inp, splits, workspace):
 
 
 @pytest.mark.gpu
+def test_noalloc_first_call_under_graph_capture(device):
+    # Defined first in the last-collected file: the process's first noalloc call
+    # happens inside the capture (nothing else calls it).  Paged decode, 8
+    # sequences, 32 / 8 heads, 4 splits; the graph is replayed three times with
+    # new lengths (eager copies and a synchronisation between replays), each
+    # replay against fa_fwd_kvcache with a caller workspace on the same inputs.
+    g = torch.Generator().manual_seed(9902)
+    q, k, v, kc, vc, table, lens = _inputs(g, 8, 1, 32, 8, 128, 2048, True)
+    splits = 4
+    qd, kd, vd, td = q.to(device), k.to(device), v.to(device), table.to(device)
+    kc0, vc0 = kc.to(device), vc.to(device)
+    kcd, vcd = kc0.clone(), vc0.clone()
+    seq_d = lens.to(device)
+    o = torch.zeros_like(qd)
+    lse = torch.zeros((8, 32, 1), dtype=torch.float32, device=device)
+    a = fa_capi.kvcache_args(qd, kcd, vcd, o, lse, seq_d, 128 ** -0.5, True, splits, kd, vd, block_table=td)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print("noalloc: first call inside torch.cuda.graph capture", flush=True)
+    with torch.cuda.graph(graph):
+        fa_capi.call("fa_fwd_kvcache_noalloc", a)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        new_lens = torch.randint(0, 2048, (8,), generator=g, dtype=torch.int32)
+        new_lens[rep] = 2047
+        seq_d.copy_(new_lens.to(device))
+        kcd.copy_(kc0)
+        vcd.copy_(vc0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _call(device, "fa_fwd_kvcache", (q, k, v, kc, vc, table, new_lens), splits, True)
+        for n, r, x in zip(("out", "lse", "k_cache", "v_cache"), ref, (o.cpu(), lse.cpu(), kcd.cpu(), vcd.cpu())):
+            assert torch.equal(r, x), f"replay {rep}: {n} differs from fa_fwd_kvcache"
+    del graph
+
+
+@pytest.mark.gpu
 def test_noalloc_matches_workspace_entry_point(device):
     g = torch.Generator().manual_seed(9900)
-    # First call: paged decode, 64 sequences, 8 splits (4.2 MB of accumulators); then a
+    # First call: paged decode, 64 sequences, 8 splits (8.5 MB of accumulators); then a
     # smaller contiguous multi-token call over the same scratch; then one split.
     runs = [
         (_inputs(g, 64, 1, 32, 8, 128, 4096, True), 8),
