@@ -43,17 +43,16 @@ struct FwdCfg {
     static constexpr int STAGE = 2 * TILE;        // a K tile and a V tile
 };
 
-// The running maximum m a row's probabilities P = exp2(S*c - m) are taken
-// against is raised (and O, l rescaled) only in the blocks where some row of
-// the wave finds a score more than kRescaleSlack above it, so most blocks skip
-// the rescale; P then stays below 2^kRescaleSlack, well inside fp16.  O is
-// normalised by the sum of the fp16-rounded P that the PV product used
-// (l_o), so O = sum P V / l_o is built from consistent weights: a row
-// dominated by one key returns that key's V exactly whatever the stale
-// maximum, as it does with P = 1 in the reference.  The LSE uses the fp32 sum
-// of the unrounded P (l_p), as the reference does.
-constexpr float kRescaleSlack = 8.f;
-constexpr float kRescaleLimit = 256.f;  // 2^kRescaleSlack
+// Each row's probabilities P = exp2(S*c - m) are taken against its exact
+// running maximum m, as in the reference's online softmax: the block that
+// raises some row's maximum rescales O and the row sums of the wave (by 1 for
+// the rows whose maximum stands), so a row's largest score gives P = 1 exactly
+// and no P exceeds 1.  (Raising m only when a score outgrows it by 2^8 skips
+// most rescales but rounds the dominant keys' P to fp16 at up to 2^8, which
+// doubles the output error of rows dominated by a few keys.)  O is normalised
+// by the sum of the fp16-rounded P that the PV product used (l_o), so O =
+// sum P V / l_o is built from consistent weights; the LSE uses the fp32 sum of
+// the unrounded P (l_p), as the reference does.
 
 // Sum of the eight fp16 values of an MFMA operand, accumulated in fp32.
 __device__ __forceinline__ float sum8(const f16x8 &v, float acc) {
@@ -178,7 +177,7 @@ struct SoftmaxRow {
 
 // One 64-key block of S^T (two 32 x 32 accumulator tiles) -> P^T operands:
 // mask (MASK: keys past lim, relative to the block start), running maximum,
-// lazy rescale of O, exponentials, row sums.
+// rescale of O, exponentials, row sums.
 template <int HD, bool MASK>
 __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f32x16 (&o)[HD / 32], SoftmaxRow &r,
                                               float cscale, int lim, int hh) {
@@ -196,7 +195,7 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f3
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
     mx = max_xor32(mx);
     const float mx_t = MASK && mx == -INFINITY ? -INFINITY : mx * cscale;
-    if (__builtin_amdgcn_ballot_w64(mx_t > r.m_t + kRescaleSlack) != 0) {
+    if (__builtin_amdgcn_ballot_w64(mx_t > r.m_t) != 0) {
         const float m_new = fmaxf(r.m_t, mx_t);
         const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(r.m_t - m_new);
         r.l_p *= alpha;
@@ -225,41 +224,6 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f3
         pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
         r.l_o = sum8(pB[gg], r.l_o);
     }
-}
-
-// The same block without the row maximum, for kernels that can recompute S:
-// P = exp2(S*c - m) against the current maximum stands when every row of the
-// wave already has one and no P exceeds 2^kRescaleSlack (the row's sum of P
-// bounds each of them).  softmax_block would then not raise the maximum
-// either, so the results are the same bits (but for a score within fp32
-// rounding of the slack bound, where the two tests can decide differently and
-// both results are exact to rounding); otherwise (a row's first visible keys,
-// or a score that outgrows the maximum) S is left overwritten and the caller
-// recomputes it and runs softmax_block.  Returns true on success
-// (wave-uniform).
-template <int HD, bool MASK>
-__device__ __forceinline__ bool softmax_block_fast(f32x16 (&s)[2], f16x8 (&pB)[4], SoftmaxRow &r, float cscale,
-                                                   int lim, int hh) {
-    const bool have = r.m_t != -INFINITY;
-    const float m_use = have ? r.m_t : 0.f;
-    float rs = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            float p = exp2_fast(fmaf(s[kt][e], cscale, -m_use));
-            if constexpr (MASK) p = kt * 32 + acc_lrow(e, hh) > lim ? 0.f : p;
-            s[kt][e] = p;
-            rs += p;
-        }
-    if (__builtin_amdgcn_ballot_w64(!(have && rs <= kRescaleLimit)) != 0) return false;
-    r.l_p += rs;
-#pragma unroll
-    for (int gg = 0; gg < 4; ++gg) {
-        pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
-        r.l_o = sum8(pB[gg], r.l_o);
-    }
-    return true;
 }
 
 // Epilogue: O / l in fp16, LSE = ln(sum exp(scale*S)); empty rows give 0 / 0.
@@ -317,9 +281,7 @@ struct KvLoader {
 // 4-wave kernel: each wave runs S, softmax and PV of a block in turn; two
 // workgroups per CU at head_dim 128 (64 KB LDS, 246 registers), three at
 // head_dim 64 (32 KB LDS, at most 168 registers), overlap one wave's softmax
-// with the others' MFMAs on each SIMD.  At head_dim 64 the kernel is bound by
-// VALU work, so its blocks first try the softmax without the row maximum
-// (softmax_block_fast).
+// with the others' MFMAs on each SIMD.
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks, const int lg) {
     constexpr int NT = 256;
@@ -368,28 +330,15 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
         f32x16 s[2];
-        auto scores = [&]() FA_INLINE {
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
+        for (int kt = 0; kt < 2; ++kt) {
+            s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
 #pragma unroll
-                for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
-            }
-        };
-        scores();
+            for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
+        }
         const int lim = (CAUSAL ? min(w.sk - 1, qi + w.causal_off) : w.sk - 1) - n0;
         f16x8 pB[4];
-        // K_nb stays in this stage until the next block's barrier, so S can be
-        // recomputed when the maximum-free softmax does not stand.  Head_dim 64
-        // only: at 128 the second S product pushes the kernel into spills.
-        if constexpr (HD == 64) {
-            if (!softmax_block_fast<HD, MASK>(s, pB, row, w.cscale, lim, hh)) {
-                scores();
-                softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
-            }
-        } else {
-            softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
-        }
+        softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
