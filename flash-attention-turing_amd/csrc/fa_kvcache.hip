@@ -11,22 +11,25 @@
 // exp(lse_s - lse_total) and a row with no key gets O = 0, LSE = 0 (:697-727);
 // probabilities stay fp32 through the PV product (:599, :636-672).
 //
-// Design: one workgroup per (batch, KV head, split, 32-row tile) where the
-// rows are the q-heads of the GQA group times the query positions, so every
-// K/V byte of the split is read once.  The keys of the split are walked in
-// 32-key tiles aligned to absolute positions (a tile never straddles a page:
-// pages are multiples of 256 tokens), tile t going to wave t % 4.  Each wave
+// Design: one workgroup per (batch, group of HPI adjacent KV heads, split,
+// 32-row tile) where the rows are the q-heads of the GQA group times the query
+// positions, so every K/V byte of the split is read once.  The keys of the
+// split are walked in 32-key tiles aligned to absolute positions (a tile never
+// straddles a page: pages are multiples of 256 tokens); wave w serves head
+// w % HPI of the group and its tiles t with t % (4 / HPI) == w / HPI (HPI = 1:
+// one head, tile t to wave t % 4).  Each wave
 // streams its tiles through a private LDS slot with direct global -> LDS
 // copies (global_load_lds): it reads a tile's MFMA operands into registers,
 // issues the next tile's copy into the same slot and then computes, so the
 // copy is in flight during the compute, with no register staging of the copy
 // and no workgroup barrier in the loop.  K stays natural (MFMA A operand
 // rows), V natural and read transposed with ds_read_b64_tr_b16.  Each wave
-// keeps its own online softmax state; the four waves merge their partial
-// states through LDS at the end.  Paged, remapped and contiguous caches take
-// the same tile order and the same arithmetic, so their results are
-// bit-identical for the same logical cache.  Work items are ordered with the
-// sequence rank slowest: when the caller passes a batch_order workspace, one
+// keeps its own online softmax state; the waves of each head merge their
+// partial states through LDS at the end.  Paged, remapped and contiguous
+// caches with the same head stride take the same tile order and the same
+// arithmetic, so their results are bit-identical for the same logical cache.
+// Work items are ordered with the sequence rank slowest: when the caller
+// passes a batch_order workspace, one
 // workgroup of the append launch first ranks the sequences by key count
 // (longest first) and a resident grid of two workgroups per CU deals the items
 // out from a device counter in that order, so the longest sequences start
@@ -351,10 +354,16 @@ __device__ __forceinline__ float tanh_fast(float x) {
 // the tile's rows with combine_row, as the combine kernel would.
 // EXT switches on the local window, softcap, ALiBi, cache_leftpad and rotary options
 // (a separate instance, so the plain kernel carries none of their work).
-template <int HD, bool DYN, bool EXT>
+// HPI (1, 2 or 4) KV heads per item: wave w serves head hk0 + w % HPI and
+// takes every (4 / HPI)-th tile of it, so at one key position the waves of a
+// workgroup read HPI adjacent heads' rows, HPI * head_dim * 2 contiguous bytes
+// of a head-interleaved cache row, where one head alone reads 128 or 256.
+template <int HD, bool DYN, bool EXT, int HPI>
 __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_args a, const int row_tiles,
                                                             const int n_items, int32_t *const count) {
     using C = KvCfg<HD>;
+    static_assert(HPI == 1 || HPI == 2 || HPI == 4, "heads per item");
+    constexpr int WPH = kKvWaves / HPI;  // waves per head
     __shared__ __attribute__((aligned(16))) char smem[kKvWaves * C::WAVE_LDS + kKvWaves * 2 * 32 * 4];
     __shared__ int pages[C::MAX_PAGES];
     __shared__ int next_item, last_item;
@@ -362,12 +371,14 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int col = lane & 31, hh = lane >> 5;
+    const int n_groups = a.nheads_k / HPI;
     for (int item = blockIdx.x; item < n_items;) {
         int rest = item;
         const int rt = rest % row_tiles;
         rest /= row_tiles;
-        const int hk = rest % a.nheads_k;
-        rest /= a.nheads_k;
+        const int hk0 = (rest % n_groups) * HPI;  // the item's first KV head
+        const int hk = hk0 + wave % HPI;          // this wave's
+        rest /= n_groups;
         const int split = rest % a.num_splits;
         const int rank = rest / a.num_splits;
         const int b = a.batch_order ? a.batch_order[rank] : rank;
@@ -454,8 +465,8 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
 
         const int t_first = k_lo / kTile;
         const int t_last = k_hi > k_lo ? (k_hi - 1) / kTile : t_first - 1;
-        const int my_first = t_first + wave;
-        const int n_my = my_first <= t_last ? (t_last - my_first) / kKvWaves + 1 : 0;
+        const int my_first = t_first + wave / HPI;
+        const int n_my = my_first <= t_last ? (t_last - my_first) / WPH + 1 : 0;
 
         // Page ids of the split, staged in LDS so the ring never waits on a table read.
         const int page = a.page_block_size;
@@ -509,7 +520,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         TileReader<HD> rd;
         rd.init(lane);
         if (n_my > 0) issue(my_first, 0);
-        if (C::NST > 1 && n_my > 1) issue(my_first + kKvWaves, 1);
+        if (C::NST > 1 && n_my > 1) issue(my_first + WPH, 1);
         for (int k = 0; k < n_my; ++k) {
             const int st = k % C::NST;
             if (k + 1 < n_my)
@@ -518,7 +529,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
                 wait_vmem();
             const char *ks = smem + (wave * C::NST + st) * C::STAGE;
             const char *vs = ks + C::TILE;
-            const int p0 = (my_first + k * kKvWaves) * kTile;
+            const int p0 = (my_first + k * WPH) * kTile;
             // All operands of the tile into registers first, then refill the stage
             // right away: two tiles stay in flight while this one is computed.
             f16x8 ka[HD / 16], va[HD / 32][2];
@@ -529,7 +540,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
     #pragma unroll
                 for (int gg = 0; gg < 2; ++gg) va[dt][gg] = rd.tr_operand(vs, 16 * gg, dt);
             wait_lds();
-            if (k + C::NST < n_my) issue(my_first + (k + C::NST) * kKvWaves, st);
+            if (k + C::NST < n_my) issue(my_first + (k + C::NST) * WPH, st);
             f32x16 s = mfma32(ka[0], qB[0], zero16());
     #pragma unroll
             for (int g = 1; g < HD / 16; ++g) s = mfma32(ka[g], qB[g], s);
@@ -605,7 +616,8 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
         else
             run(std::false_type{});
 
-        // Merge the four waves: each publishes (m, l) per row and its O^T tile.
+        // Merge the waves of each head (waves j, j + HPI, ...): each publishes
+        // (m, l) per row and its O^T tile.
         const float l_w = sum_xor32(l_p);
         float *mrow = reinterpret_cast<float *>(smem + kKvWaves * C::WAVE_LDS);
         float *lrow = mrow + kKvWaves * 32;
@@ -623,15 +635,16 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
 
         const int rows_here = min(32, R - rt * 32);
         const int nrow_all = a.batch * a.nheads * a.seqlen_q;
-        for (int e = tid; e < rows_here * HD; e += kKvThreads) {
-            const int c = e / HD, d = e % HD;
+        for (int e = tid; e < HPI * rows_here * HD; e += kKvThreads) {
+            const int j = e / (rows_here * HD), c = (e / HD) % rows_here, d = e % HD;
             float mstar = -INFINITY;
     #pragma unroll
-            for (int w = 0; w < kKvWaves; ++w) mstar = fmaxf(mstar, mrow[w * 32 + c]);
+            for (int i = 0; i < WPH; ++i) mstar = fmaxf(mstar, mrow[(j + HPI * i) * 32 + c]);
             float lsum = 0.f, acc = 0.f;
             if (mstar != -INFINITY) {
     #pragma unroll
-                for (int w = 0; w < kKvWaves; ++w) {
+                for (int i = 0; i < WPH; ++i) {
+                    const int w = j + HPI * i;
                     const float mw = mrow[w * 32 + c];
                     const float sc = mw == -INFINITY ? 0.f : exp2_fast(mw - mstar);
                     lsum += lrow[w * 32 + c] * sc;
@@ -642,7 +655,7 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
             const float outv = live ? acc / lsum : 0.f;
             const float lse = live ? (mstar + log2_fast(lsum)) * kLn2 : -INFINITY;
             const int r = rt * 32 + c;
-            const int qp = r / G, h = hk * G + r % G;
+            const int qp = r / G, h = (hk0 + j) * G + r % G;
             const int64_t orow = (int64_t(b) * a.nheads + h) * a.seqlen_q + qp;  // (batch, head, qpos)
             if (S == 1) {
                 f16 *op = (f16 *)a.o.ptr + int64_t(b) * a.o.batch_stride + int64_t(qp) * a.o.row_stride +
@@ -669,17 +682,18 @@ __global__ __launch_bounds__(256, 2) void kv_splitkv_kernel(const fa_kvcache_arg
             // model (the atomics are relaxed): an agent-scope store is written
             // past the XCD's L2 before its vmcnt completes, and an agent-scope
             // load does not hit another XCD's stale L2 copy; the #error at the
-            // top of this file keeps other targets from building it.
+            // top of this file keeps other targets from building it.  The count
+            // of a row tile of a head group sits at its first head's slot.
             wait_vmem();
             __syncthreads();
             if (tid == 0)
-                last_item = __hip_atomic_fetch_add(count + (int64_t(b) * a.nheads_k + hk) * row_tiles + rt, 1,
+                last_item = __hip_atomic_fetch_add(count + (int64_t(b) * a.nheads_k + hk0) * row_tiles + rt, 1,
                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
             __syncthreads();
             if (last_item) {
-                for (int c = wave; c < rows_here; c += kKvWaves) {
-                    const int r = rt * 32 + c;
-                    combine_row<HD, true>(a, (b * a.nheads + hk * G + r % G) * a.seqlen_q + r / G, lane);
+                for (int c = wave; c < HPI * rows_here; c += kKvWaves) {
+                    const int j = c / rows_here, r = rt * 32 + c % rows_here;
+                    combine_row<HD, true>(a, (b * a.nheads + (hk0 + j) * G + r % G) * a.seqlen_q + r / G, lane);
                 }
             }
         }
@@ -810,11 +824,29 @@ int launch_prep(const fa_kvcache_args &a, bool append, bool order, hipStream_t s
     return int(hipGetLastError());
 }
 
+// KV heads per work item of the resident split kernel without options: in a
+// head-interleaved cache (head stride = head_dim) enough adjacent heads that
+// one key position's rows of an item are 512 contiguous bytes (HBM reads of
+// 128-byte pieces at a 2 KB stride run about 10 % below 512-byte ones on
+// MI355X), while the items still number at least two per CU.
+int kv_heads_per_item(const fa_kvcache_args &a) {
+    const bool interleaved = a.k_cache.head_stride == a.head_dim && a.v_cache.head_stride == a.head_dim;
+    const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
+    if (!a.batch_order || ext || !interleaved) return 1;
+    const int64_t items = split_items(a);
+    int hpi = 1;
+    while (hpi < 4 && int64_t(a.head_dim) * 2 * (2 * hpi) <= 512 && a.nheads_k % (2 * hpi) == 0 &&
+           items / (2 * hpi) >= 2 * int64_t(device_cus()))
+        hpi *= 2;
+    return hpi;
+}
+
 // The split kernel.  With batch_order (ranked and its counter reset by
 // launch_prep on the same stream): a resident grid of two workgroups per CU
 // that deals the items out in that order.  Without it: one workgroup per item.
 int launch_split(const fa_kvcache_args &a, hipStream_t s) {
-    const int64_t gx = split_items(a);
+    const int hpi = kv_heads_per_item(a);
+    const int64_t gx = split_items(a) / hpi;
     if (gx == 0) return FA_OK;
     const int row_tiles = ((a.nheads / a.nheads_k) * a.seqlen_q + 31) / 32;
     const int n_items = int(gx);
@@ -822,22 +854,27 @@ int launch_split(const fa_kvcache_args &a, hipStream_t s) {
     const unsigned grid = unsigned(dyn ? std::min<int64_t>(gx, 2 * int64_t(device_cus())) : gx);
     int32_t *count = fused_combine(a) ? a.split_count : nullptr;
     const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
-    auto go = [&](auto hd_tag, auto dyn_tag, auto ext_tag) {
-        constexpr int HD = decltype(hd_tag)::value;
+    auto go = [&](auto hd_tag, auto dyn_tag, auto ext_tag, auto hpi_tag) {
+        constexpr int HD = decltype(hd_tag)::value, HPI = decltype(hpi_tag)::value;
         constexpr bool DYN = decltype(dyn_tag)::value, EXT = decltype(ext_tag)::value;
-        hipLaunchKernelGGL((kv_splitkv_kernel<HD, DYN, EXT>), dim3(grid), dim3(kKvThreads), 0, s, a, row_tiles,
+        hipLaunchKernelGGL((kv_splitkv_kernel<HD, DYN, EXT, HPI>), dim3(grid), dim3(kKvThreads), 0, s, a, row_tiles,
                            n_items, count);
     };
     using H128 = std::integral_constant<int, 128>;
     using H64 = std::integral_constant<int, 64>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P4 = std::integral_constant<int, 4>;
     using T = std::true_type;
     using F = std::false_type;
     if (a.head_dim == 128) {
-        if (dyn) ext ? go(H128{}, T{}, T{}) : go(H128{}, T{}, F{});
-        else ext ? go(H128{}, F{}, T{}) : go(H128{}, F{}, F{});
+        if (dyn && !ext) hpi == 2 ? go(H128{}, T{}, F{}, P2{}) : go(H128{}, T{}, F{}, P1{});
+        else if (dyn) go(H128{}, T{}, T{}, P1{});
+        else ext ? go(H128{}, F{}, T{}, P1{}) : go(H128{}, F{}, F{}, P1{});
     } else {
-        if (dyn) ext ? go(H64{}, T{}, T{}) : go(H64{}, T{}, F{});
-        else ext ? go(H64{}, F{}, T{}) : go(H64{}, F{}, F{});
+        if (dyn && !ext) hpi == 4 ? go(H64{}, T{}, F{}, P4{}) : hpi == 2 ? go(H64{}, T{}, F{}, P2{}) : go(H64{}, T{}, F{}, P1{});
+        else if (dyn) go(H64{}, T{}, T{}, P1{});
+        else ext ? go(H64{}, F{}, T{}, P1{}) : go(H64{}, F{}, F{}, P1{});
     }
     return int(hipGetLastError());
 }

@@ -168,3 +168,39 @@ def test_kvcache_page_sizes_and_scales(device, page, hd, splits, scale):
     if splits > 1:
         contiguous = _run(device, q, kc, vc, k, v, seqlens, None, None, True, splits, scale)
         assert torch.equal(contiguous[0], out) and torch.equal(contiguous[1], lse)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,h,hk,hd", [(16, 16, 16, 64), (8, 16, 16, 64), (16, 32, 8, 128)])
+def test_kvcache_heads_per_item(device, b, h, hk, hd):
+    """Decode calls with enough work items (2048 / 1024 / 1024 with 8 splits on
+    a 256-CU MI355X) that the split kernel gives each item 4, 2 and 2 adjacent
+    KV heads of a head-interleaved cache: append bit-exact and attention within
+    2x the reference's error against the oracle; the paged copy of the cache
+    (also head-interleaved, so the same grouping) bit-identical; the same
+    logical cache stored heads-major (one head per item) within the same bound."""
+    g = torch.Generator().manual_seed(7000 + b + hk + hd)
+    cap, splits = 1024, 8
+    kc = randn16((b, cap, hk, hd), g)
+    vc = randn16((b, cap, hk, hd), g)
+    q = randn16((b, 1, h, hd), g)
+    k = randn16((b, 1, hk, hd), g)
+    v = randn16((b, 1, hk, hd), g)
+    seqlens = torch.randint(256, cap, (b,), generator=g, dtype=torch.int32)
+    seqlens[0] = cap - 1
+    out, lse, kc_after, vc_after = _run(device, q, kc, vc, k, v, seqlens, None, None, True, splits)
+    o_ref, l_ref, kc_ref, vc_ref = _oracle(q, kc, vc, k, v, seqlens, None, None, True, splits, None)
+    assert torch.equal(kc_after, kc_ref) and torch.equal(vc_after, vc_ref)
+    assert_2x("out", out, o_ref, o_ref.to(torch.float16))
+    assert_lse(lse, l_ref)
+    kp, vp, table = _paged_from_contiguous(kc, vc, seqlens, 256, g)
+    paged = _run(device, q, kp, vp, k, v, seqlens, None, table, True, splits)
+    assert torch.equal(paged[0], out) and torch.equal(paged[1], lse)
+    # [b][hk][cap][d] storage seen as a strided [b][cap][hk][d] cache
+    kh = kc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    vh = vc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    assert kh.stride(2) == cap * hd
+    heads_major = _run(device, q, kh, vh, k, v, seqlens, None, None, True, splits)
+    assert torch.equal(heads_major[2], kc_ref) and torch.equal(heads_major[3], vc_ref)
+    assert_2x("out (heads-major cache)", heads_major[0], o_ref, o_ref.to(torch.float16))
+    assert_lse(heads_major[1], l_ref)
