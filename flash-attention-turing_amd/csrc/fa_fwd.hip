@@ -49,20 +49,9 @@ struct FwdCfg {
 // the rows whose maximum stands), so a row's largest score gives P = 1 exactly
 // and no P exceeds 1.  (Raising m only when a score outgrows it by 2^8 skips
 // most rescales but rounds the dominant keys' P to fp16 at up to 2^8, which
-// doubles the output error of rows dominated by a few keys.)  O is normalised
-// by the sum of the fp16-rounded P that the PV product used (l_o), so O =
-// sum P V / l_o is built from consistent weights; the LSE uses the fp32 sum of
-// the unrounded P (l_p), as the reference does.
-
-// Sum of the eight fp16 values of an MFMA operand, accumulated in fp32.
-__device__ __forceinline__ float sum8(const f16x8 &v, float acc) {
-    typedef f16 f16x2 __attribute__((ext_vector_type(2)));
-    const f16x2 one = {f16(1), f16(1)};
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
-    return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
-}
+// doubles the output error of rows dominated by a few keys.)  As in the
+// reference, the PV product takes P rounded to fp16 and both O and the LSE
+// are normalised by the fp32 sum of the unrounded P.
 
 // Per-workgroup extents and base pointers of one (batch, query heads, block of
 // query positions).  A workgroup covers gp = 2^lg query heads of one GQA group
@@ -171,8 +160,7 @@ __device__ __forceinline__ void load_q(const fa_fwd_args &a, const FwdWork &w, i
 // Online-softmax state of a wave's 32 queries (this lane's query column).
 struct SoftmaxRow {
     float m_t = -INFINITY;  // reference max of scale*log2(e)*S for this lane's query
-    float l_p = 0.f;        // partial row sum over this lane half's keys (fp32 P, for the LSE)
-    float l_o = 0.f;        // the same over the fp16-rounded P (normalises O)
+    float l_p = 0.f;        // partial row sum over this lane half's keys (fp32 P)
 };
 
 // One 64-key block of S^T (two 32 x 32 accumulator tiles) -> P^T operands:
@@ -199,7 +187,6 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f3
         const float m_new = fmaxf(r.m_t, mx_t);
         const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(r.m_t - m_new);
         r.l_p *= alpha;
-        r.l_o *= alpha;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
@@ -222,7 +209,6 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f16x8 (&pB)[4], f3
 #pragma unroll
     for (int gg = 0; gg < 4; ++gg) {
         pB[gg] = pack8(s[gg >> 1], 8 * (gg & 1));
-        r.l_o = sum8(pB[gg], r.l_o);
     }
 }
 
@@ -231,9 +217,8 @@ template <int HD>
 __device__ __forceinline__ void store_row(const fa_fwd_args &a, const FwdWork &w, int qi, int hh,
                                           const f32x16 (&o)[HD / 32], const SoftmaxRow &r) {
     const float l_tot = sum_xor32(r.l_p);
-    const float lo_tot = sum_xor32(r.l_o);
     if (qi < w.sq) {
-        const float inv = lo_tot > 0.f ? 1.f / lo_tot : 0.f;
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
         f16 *orow = w.op + int64_t(qi) * a.o.row_stride;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
