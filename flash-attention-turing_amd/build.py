@@ -4,6 +4,8 @@ Outputs (next to this file):
   * libfa_mi355x.so   - the HIP kernels behind the C ABI of include/fa_mi355x.h
                         (hipcc --offload-arch=gfx950)
   * flash_attn_turing.<ext>.so - the Python extension module (host layer)
+  * probes/ceiling_probe - the hardware-ceiling probe (MFMA rate and clock, LDS
+                        instruction costs, HBM read rates) behind the rooflines
 
 Usage:  python build.py [--jobs N]
 """
@@ -118,9 +120,18 @@ def build_extension(out_dir: str = HERE) -> str:
     return out
 
 
+def build_probe() -> str:
+    src = os.path.join(HERE, "probes", "ceiling_probe.hip")
+    out = os.path.join(HERE, "probes", "ceiling_probe")
+    _run([HIPCC, *HIP_FLAGS, src, "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(jobs: int = 4) -> None:
     build_library(jobs)
     build_extension()
+    build_probe()
 
 
 if __name__ == "__main__":
@@ -131,4 +142,5 @@ if __name__ == "__main__":
     print("built", build_library(args.jobs))
     if not args.lib_only:
         print("built", build_extension())
+        print("built", build_probe())
     sys.exit(0)
