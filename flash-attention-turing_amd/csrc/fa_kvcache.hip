@@ -828,15 +828,17 @@ int launch_prep(const fa_kvcache_args &a, bool append, bool order, hipStream_t s
 // head-interleaved cache (head stride = head_dim) enough adjacent heads that
 // one key position's rows of an item are 512 contiguous bytes (HBM reads of
 // 128-byte pieces at a 2 KB stride run about 10 % below 512-byte ones on
-// MI355X), while the items still number at least two per CU.
+// MI355X), while every resident workgroup still gets at least four items:
+// with fewer, the items of the longest sequences (their splits are the
+// largest) decide the call's time.
 int kv_heads_per_item(const fa_kvcache_args &a) {
     const bool interleaved = a.k_cache.head_stride == a.head_dim && a.v_cache.head_stride == a.head_dim;
     const bool ext = a.local_window || a.softcap > 0.f || a.cache_leftpad || a.alibi_slopes || a.rotary_dim > 0;
     if (!a.batch_order || ext || !interleaved) return 1;
-    const int64_t items = split_items(a);
+    const int64_t items = split_items(a), slots = 2 * int64_t(device_cus());
     int hpi = 1;
     while (hpi < 4 && int64_t(a.head_dim) * 2 * (2 * hpi) <= 512 && a.nheads_k % (2 * hpi) == 0 &&
-           items / (2 * hpi) >= 2 * int64_t(device_cus()))
+           items / (2 * hpi) >= 4 * slots)
         hpi *= 2;
     return hpi;
 }

@@ -171,14 +171,15 @@ def test_kvcache_page_sizes_and_scales(device, page, hd, splits, scale):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("b,h,hk,hd", [(16, 16, 16, 64), (8, 16, 16, 64), (16, 32, 8, 128)])
+@pytest.mark.parametrize("b,h,hk,hd", [(64, 16, 16, 64), (32, 16, 16, 64), (64, 32, 8, 128)])
 def test_kvcache_heads_per_item(device, b, h, hk, hd):
-    """Decode calls with enough work items (2048 / 1024 / 1024 with 8 splits on
-    a 256-CU MI355X) that the split kernel gives each item 4, 2 and 2 adjacent
-    KV heads of a head-interleaved cache: append bit-exact and attention within
-    2x the reference's error against the oracle; the paged copy of the cache
-    (also head-interleaved, so the same grouping) bit-identical; the same
-    logical cache stored heads-major (one head per item) within the same bound."""
+    """Decode calls with enough work items (8192 / 4096 / 4096 with 8 splits on
+    a 256-CU MI355X: at least four per resident workgroup after the grouping)
+    that the split kernel gives each item 4, 2 and 2 adjacent KV heads of a
+    head-interleaved cache: append bit-exact and attention within 2x the
+    reference's error against the oracle; the paged copy of the cache (also
+    head-interleaved, so the same grouping) bit-identical; the same logical
+    cache stored heads-major (one head per item) within the same bound."""
     g = torch.Generator().manual_seed(7000 + b + hk + hd)
     cap, splits = 1024, 8
     kc = randn16((b, cap, hk, hd), g)
