@@ -266,12 +266,18 @@ struct KvLoader {
 // 4-wave kernel: each wave runs S, softmax and PV of a block in turn; two
 // workgroups per CU at head_dim 128 (64 KB LDS, 246 registers), three at
 // head_dim 64 (32 KB LDS, at most 168 registers), overlap one wave's softmax
-// with the others' MFMAs on each SIMD.
-template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd_args a, const int num_m_blocks, const int lg) {
+// with the others' MFMAs on each SIMD.  QT = 2 (head_dim 64): each wave takes
+// two 32-query tiles of one head and each K / V operand it reads from LDS
+// feeds both tiles' MFMAs, which halves the LDS reads per MFMA (the kernel's
+// bound at head_dim 64, where a score costs half the MFMA work for the same
+// reads of V); two workgroups of 256 queries per CU.  The per-tile arithmetic
+// is the same, so the results are the same bits.
+template <int HD, bool CAUSAL, int QT>
+__global__ __launch_bounds__(256, QT == 2 || HD == 128 ? 2 : 3) void fwd_kernel(const fa_fwd_args a,
+                                                                                const int num_m_blocks, const int lg) {
     constexpr int NT = 256;
     using C = FwdCfg<HD, NT>;
-    constexpr int BM = C::BM, BN = C::BN;
+    constexpr int BM = C::BM * QT, BN = C::BN;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -280,16 +286,23 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd
     FwdWork w;
     if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, lg, w)) return;
 
-    const int q_lo = fwd_wave(a, w, wave);
-    const int qi = q_lo + (lane & 31);
-    f16x8 qB[HD / 16];
-    load_q<HD>(a, w, qi, hh, qB);
+    // The wave's tiles QT * wave + t: one head (a head spans at least 64 positions when QT = 2).
+    const int q_lo = fwd_wave(a, w, QT * wave);
+    int qi[QT];
+    f16x8 qB[QT][HD / 16];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        qi[t] = q_lo + 32 * t + (lane & 31);
+        load_q<HD>(a, w, qi[t], hh, qB[t]);
+    }
     wait_vmem();  // only the tile copies are in flight inside the loop
 
-    f32x16 o[HD / 32];
+    f32x16 o[QT][HD / 32];
 #pragma unroll
-    for (int i = 0; i < HD / 32; ++i) o[i] = zero16();
-    SoftmaxRow row;
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i) o[t][i] = zero16();
+    SoftmaxRow row[QT];
 
     TileReader<HD> rd;
     rd.init(lane);
@@ -302,7 +315,9 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd
 
     // One key block: S^T = K Q^T, online softmax, O^T += V^T P^T.  MASK is a
     // compile-time switch so the blocks away from the causal diagonal and
-    // the sequence end carry no masking work at all.
+    // the sequence end carry no masking work at all.  A tile with no visible
+    // key in a block it shares with the wave's other tile gets P = 0 there
+    // (its O, sums and maximum unchanged).
     auto block = [&](int nb, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = nb & 1;
@@ -310,24 +325,66 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd
         __syncthreads();  // block nb is in LDS; every wave is done with stage buf ^ 1
         if (nb + 1 < w.n_blocks) issue(nb + 1, buf ^ 1);
         const int n0 = nb * BN;
-        if (CAUSAL && MASK && n0 > q_lo + 31 + w.causal_off) return;  // no visible key for this wave
-        if (q_lo >= w.sq) return;                                      // no query row of the sequence
+        if (CAUSAL && MASK && n0 > q_lo + 32 * QT - 1 + w.causal_off) return;  // no visible key for this wave
+        if (q_lo >= w.sq) return;                                               // no query row of the sequence
         const char *ks = smem + buf * C::STAGE;
         const char *vs = ks + C::TILE;
-        f32x16 s[2];
+        f32x16 s[QT][2];
+        f16x8 pB[QT][4];
+        auto softmax = [&]() FA_INLINE {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            s[kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0], zero16());
+            for (int t = 0; t < QT; ++t) {
+                const int lim = (CAUSAL ? min(w.sk - 1, qi[t] + w.causal_off) : w.sk - 1) - n0;
+                softmax_block<HD, MASK>(s[t], pB[t], o[t], row[t], w.cscale, lim, hh);
+            }
+        };
+        if constexpr (QT == 1) {
 #pragma unroll
-            for (int g = 1; g < HD / 16; ++g) s[kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[g], s[kt]);
+            for (int kt = 0; kt < 2; ++kt) {
+                s[0][kt] = mfma32(rd.a_operand(ks, 32 * kt, 0), qB[0][0], zero16());
+#pragma unroll
+                for (int g = 1; g < HD / 16; ++g) s[0][kt] = mfma32(rd.a_operand(ks, 32 * kt, g), qB[0][g], s[0][kt]);
+            }
+            softmax();
+#pragma unroll
+            for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) o[0][dt] = mfma32(rd.tr_operand(vs, 16 * gg, dt), pB[0][gg], o[0][dt]);
+        } else {
+            // Each operand feeds both tiles' MFMAs.  The reads run PIPE steps
+            // ahead behind scheduling fences (all of them hoisted to the top
+            // would not fit the registers of two waves per SIMD), from an opaque
+            // copy of the lane's base offsets (hoisted out of the loop, the
+            // per-read addresses would hold registers for the whole kernel).
+            constexpr int PIPE = 3, NS = 2 * (HD / 16), NPV = 4 * (HD / 32);
+            TileReader<HD> r = rd;
+            asm volatile("" : "+v"(r.a_base), "+v"(r.tr_base[0]), "+v"(r.tr_base[1]));
+            f16x8 op[PIPE];
+            auto rd_k = [&](int u) FA_INLINE { op[u % PIPE] = r.a_operand(ks, 32 * (u / (HD / 16)), u % (HD / 16)); };
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < PIPE - 1; ++u) rd_k(u);
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+                if (u + PIPE - 1 < NS) rd_k(u + PIPE - 1);
+                const int kt = u / (HD / 16), g = u % (HD / 16);
+#pragma unroll
+                for (int t = 0; t < QT; ++t) s[t][kt] = mfma32(op[u % PIPE], qB[t][g], g == 0 ? zero16() : s[t][kt]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            softmax();
+            auto rd_v = [&](int u) FA_INLINE { op[u % PIPE] = r.tr_operand(vs, 16 * (u & 3), u >> 2); };
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < PIPE - 1; ++u) rd_v(u);
+#pragma unroll
+            for (int u = 0; u < NPV; ++u) {
+                if (u + PIPE - 1 < NPV) rd_v(u + PIPE - 1);
+#pragma unroll
+                for (int t = 0; t < QT; ++t) o[t][u >> 2] = mfma32(op[u % PIPE], pB[t][u & 3], o[t][u >> 2]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        const int lim = (CAUSAL ? min(w.sk - 1, qi + w.causal_off) : w.sk - 1) - n0;
-        f16x8 pB[4];
-        softmax_block<HD, MASK>(s, pB, o, row, w.cscale, lim, hh);
-#pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) o[dt] = mfma32(rd.tr_operand(vs, 16 * gg, dt), pB[gg], o[dt]);
     };
 
     // Blocks [0, n_full) need no mask for any wave of the workgroup: every key
@@ -337,7 +394,8 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void fwd_kernel(const fa_fwd
     if (w.n_blocks > 0) issue(0, 0);
     for (int nb = 0; nb < n_full; ++nb) block(nb, std::false_type{});
     for (int nb = n_full; nb < w.n_blocks; ++nb) block(nb, std::true_type{});
-    store_row<HD>(a, w, qi, hh, o, row);
+#pragma unroll
+    for (int t = 0; t < QT; ++t) store_row<HD>(a, w, qi[t], hh, o[t], row[t]);
 }
 
 // ---------------------------------------------------------------------------
@@ -567,6 +625,21 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
             return int(hipGetLastError());
         }
     }
+    // Head_dim 64: two query tiles per wave when that grid still fills the chip twice over.
+    if constexpr (HD == 64) {
+        constexpr int BM2 = 2 * FwdCfg<HD, 256>::BM;
+        const int lg = fwd_pack_log2(a, BM2), P = BM2 >> lg;
+        const int64_t m_blocks = (a.lse_seqlen + P - 1) / P;
+        const int64_t grid = m_blocks * a.batch * (a.nheads >> lg);
+        if (grid >= 2 * int64_t(device_cus())) {
+            if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
+            const int rc = launch_order(a, int(m_blocks), P, stream);
+            if (rc) return rc;
+            hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL, 2>), dim3(unsigned(grid)), dim3(256), 0, stream, a,
+                               int(m_blocks), lg);
+            return int(hipGetLastError());
+        }
+    }
     constexpr int BM = FwdCfg<HD, 256>::BM;
     const int lg = fwd_pack_log2(a, BM), P = BM >> lg;
     const int num_m_blocks = (a.lse_seqlen + P - 1) / P;
@@ -575,7 +648,7 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
     if (grid > 0x7fffffff) return FA_ERR_INVALID_ARG;
     const int rc = launch_order(a, num_m_blocks, P, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL>), dim3(unsigned(grid)), dim3(256), 0, stream, a, num_m_blocks, lg);
+    hipLaunchKernelGGL((fwd_kernel<HD, CAUSAL, 1>), dim3(unsigned(grid)), dim3(256), 0, stream, a, num_m_blocks, lg);
     return int(hipGetLastError());
 }
 
