@@ -59,10 +59,10 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 # profiles/hbm_bytes_pmc.md.  Re-measured whenever a kernel changes; None
 # where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 4.522e8 + 6.881e7,
-    "bwd_dq": 6.359e8 + 7.349e7,
-    "bwd_dkdv": 7.494e8 + 1.413e8,
-    "kv_splitkv": 4.706e9 + 9.717e6,
+    "fwd": 4.586e8 + 6.895e7,
+    "bwd_dq": 7.825e8 + 6.931e7,
+    "bwd_dkdv": 7.395e8 + 1.462e8,
+    "kv_splitkv": 4.705e9 + 9.581e6,
 }
 
 
