@@ -286,7 +286,8 @@ __global__ __launch_bounds__(256, QT == 2 || HD == 128 ? 2 : 3) void fwd_kernel(
     FwdWork w;
     if (!fwd_work<BM, CAUSAL>(a, num_m_blocks, lg, w)) return;
 
-    // The wave's tiles QT * wave + t: one head (a head spans at least 64 positions when QT = 2).
+    // The wave's tiles QT * wave + t: one head (the launcher packs at most BM / 64 heads when QT = 2,
+    // so a head spans at least 64 positions).
     const int q_lo = fwd_wave(a, w, QT * wave);
     int qi[QT];
     f16x8 qB[QT][HD / 16];
@@ -625,10 +626,12 @@ static int launch_fwd(const fa_fwd_args &a, hipStream_t stream) {
             return int(hipGetLastError());
         }
     }
-    // Head_dim 64: two query tiles per wave when that grid still fills the chip twice over.
+    // Head_dim 64: two query tiles per wave when that grid still fills the chip
+    // twice over.  A wave's two tiles must be one head's, so at most 4 heads
+    // share a workgroup (64 positions each).
     if constexpr (HD == 64) {
         constexpr int BM2 = 2 * FwdCfg<HD, 256>::BM;
-        const int lg = fwd_pack_log2(a, BM2), P = BM2 >> lg;
+        const int lg = min(fwd_pack_log2(a, BM2), 2), P = BM2 >> lg;
         const int64_t m_blocks = (a.lse_seqlen + P - 1) / P;
         const int64_t grid = m_blocks * a.batch * (a.nheads >> lg);
         if (grid >= 2 * int64_t(device_cus())) {

@@ -57,7 +57,9 @@ LARGE = [
     (4, 2300, 1900, 16, 8, 128, True),   # ping-pong, 2 heads x 128 positions
     (2, 4096, 4096, 32, 8, 128, False),  # ping-pong, 4 heads x 64 positions
     (2, 1500, 1500, 32, 4, 128, True),   # 128-row kernel, 4 heads x 32 positions
-    (4, 3000, 3000, 32, 8, 64, True),    # head_dim 64 (128-row kernel)
+    (4, 3000, 3000, 32, 8, 64, True),    # head_dim 64, two query tiles per wave, 4 heads x 64 positions
+    (4, 2048, 2048, 16, 2, 64, True),    # head_dim 64, groups of 8: still 4 heads x 64 positions
+    (4, 2048, 1900, 16, 1, 64, False),   # head_dim 64, one kv head (group 16), sq != sk
 ]
 
 
@@ -80,6 +82,8 @@ def test_gqa_pack_large_bitwise(device, b, sq, sk, h, hk, hd, causal):
 @pytest.mark.parametrize("lens_q,lens_k,h,hk,hd,causal", [
     ([300, 0, 1, 77, 31, 33], None, 16, 2, 128, True),
     ([200, 17, 90, 64], [100, 300, 90, 0], 8, 2, 64, False),
+    # head_dim 64 with a grid large enough for two query tiles per wave, groups of 8
+    ([1900, 1200, 2048, 700, 1500, 1000, 1800, 2000], None, 16, 2, 64, True),
 ])
 def test_gqa_pack_varlen(device, lens_q, lens_k, h, hk, hd, causal):
     """Packed sequences with empty and one-row members: every head of a pack
