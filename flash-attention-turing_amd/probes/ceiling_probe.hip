@@ -6,11 +6,17 @@
 //     SIMD, and with 64 queries per wave (each operand read feeds two MFMAs);
 //   * LDS instruction costs per CU with many reads / writes in flight:
 //     ds_read_b128, ds_read_b64_tr_b16, ds_write_b128, ds_write_b64;
+//   * VALU issue costs: v_exp_f32 alone, v_fma_f32 alone, the two interleaved,
+//     and v_exp_f32 beside MFMAs of the same wave (the softmax's mix);
 //   * HBM read bandwidth: contiguous, and in 128 / 256 / 512-byte pieces at a
 //     2 KB stride (one / two / four heads of a head-interleaved KV cache row).
 // Timing only.  Every LDS address stays inside the workgroup's buffer and every
-// global address inside the allocation; every loop is bounded.  The clock is
-// read inside the kernel: s_memtime (shader cycles) over s_memrealtime (100 MHz).
+// global address inside the allocation; every loop is bounded.  The on-chip probes
+// time their loops from inside: each wave stamps s_memrealtime (100 MHz) and
+// s_memtime (shader cycles) around its loop, and a rate is taken over the span from
+// the first wave's start to the last wave's end, at the clock those stamps give.
+// (Event time over the whole launch also counts the operand set-up before the
+// loops, which in an earlier form of this file was most of a millisecond.)
 //
 // Build: build.py compiles it to probes/ceiling_probe.  Run: ceiling_probe [iters].
 #include <hip/hip_runtime.h>
@@ -58,10 +64,14 @@ enum Mode {
     kReadTr,        // 32 ds_read_b64_tr_b16 in flight per step
     kWriteB128,     // 16 ds_write_b128 per step
     kWriteB64,      // 16 ds_write_b64 per step
+    kExp,           // 32 v_exp_f32 per step, 8 independent chains
+    kFma,           // 32 v_fma_f32 per step, 8 independent chains
+    kExpFma,        // 32 v_exp_f32 and 32 v_fma_f32 per step, interleaved
+    kMfmaExp,       // 16 MFMAs (register operands) and 32 v_exp_f32 per step in the same wave
 };
 
 struct Stamp {
-    long long cycles, ticks;  // s_memtime and s_memrealtime spans of wave 0
+    long long cycles, t0, t1;  // s_memtime span and s_memrealtime start / end of one wave's loop
 };
 
 template <int MODE, int NT>
@@ -73,22 +83,30 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
         const unsigned h = (unsigned(i) * 2654435761u) ^ (unsigned(i) >> 7);
         reinterpret_cast<f16 *>(smem)[i] = f16(float(int(h % 2001u) - 1000) * 0.001f);
     }
-    __syncthreads();
-    long long c0 = 0, r0 = 0;
-    if (tid == 0) {
-        c0 = __builtin_amdgcn_s_memtime();
-        r0 = __builtin_amdgcn_s_memrealtime();
-    }
+    // Operands with constant indices only (fully unrolled), so they live in registers.
     f16x8 q[8], p[4];
+#pragma unroll
     for (int i = 0; i < 8; ++i)
+#pragma unroll
         for (int e = 0; e < 8; ++e) q[i][e] = f16(0.01f * float(((lane * 37 + i * 11 + e * 7) % 201) - 100));
+#pragma unroll
     for (int i = 0; i < 4; ++i)
+#pragma unroll
         for (int e = 0; e < 8; ++e) p[i][e] = f16(0.01f * float(((lane * 53 + i * 13 + e * 5) % 199) - 99));
     f32x16 o[4], s[2], o2[4], s2[2];
+    float ex[8], fx[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ex[c] = fx[c] = 0.25f + 0.01f * float(c + (lane & 7));
+#pragma unroll
     for (int i = 0; i < 4; ++i)
+#pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] = o2[i][e] = 0.f;
+#pragma unroll
     for (int i = 0; i < 2; ++i)
+#pragma unroll
         for (int e = 0; e < 16; ++e) s[i][e] = s2[i][e] = 0.f;
+    __syncthreads();
+    const long long c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
     // Tiles swizzled as the kernels' are: 16-byte chunk c of row r at c ^ (r & 15) (256-byte rows),
     // or c ^ ((r >> 1) & 7) for the 128-byte rows of a transposed V tile.
     const int arow = lane & 31;
@@ -166,6 +184,22 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
                 *reinterpret_cast<f16x8 *>(const_cast<char *>(vs) + (t >> 3) * 8192 + (abase ^ ((t & 7) << 5))) = v;
             }
             asm volatile("" ::: "memory");
+        } else if constexpr (MODE == kExp || MODE == kFma || MODE == kExpFma) {
+            // exp2(-x) converges to ~0.64 and x * 0.999 + 0.001 to 1: the values stay finite.
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    if constexpr (MODE != kFma) ex[c] = __builtin_amdgcn_exp2f(-ex[c]);
+                    if constexpr (MODE != kExp) fx[c] = __builtin_fmaf(fx[c], 0.999f, 0.001f);
+                }
+        } else if constexpr (MODE == kMfmaExp) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                o[t & 3] = mfma(q[t & 7], p[t & 3], o[t & 3]);
+                ex[(2 * t) & 7] = __builtin_amdgcn_exp2f(-ex[(2 * t) & 7]);
+                ex[(2 * t + 1) & 7] = __builtin_amdgcn_exp2f(-ex[(2 * t + 1) & 7]);
+            }
         } else {
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
@@ -176,9 +210,9 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
             asm volatile("" ::: "memory");
         }
     }
-    if (tid == 0) {
-        stamp[blockIdx.x].cycles = __builtin_amdgcn_s_memtime() - c0;
-        stamp[blockIdx.x].ticks = __builtin_amdgcn_s_memrealtime() - r0;
+    {
+        const long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+        if (lane == 0) stamp[blockIdx.x * (NT / 64) + (tid >> 6)] = Stamp{c1 - c0, r0, r1};
     }
     float acc = 0.f;
     for (int i = 0; i < 4; ++i)
@@ -187,6 +221,7 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
         for (int e = 0; e < 16; ++e) acc += s[i][e] + s2[i][e];
     for (int i = 0; i < 4; ++i)
         for (int e = 0; e < 8; ++e) acc += float(p[i][e]);
+    for (int c = 0; c < 8; ++c) acc += ex[c] + fx[c];
     // Read the tiles back so the write probes' stores stay live.
     __syncthreads();
     for (int i = tid; i < kLdsUsed / 2; i += NT) acc += float(reinterpret_cast<const f16 *>(smem)[i]);
@@ -194,49 +229,52 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
 }
 
 struct Timing {
-    float ms;
-    double ghz;  // shader clock of the run (mean over workgroups)
+    double ms;   // first wave's loop start to last wave's loop end
+    double ghz;  // shader clock over the loops (all waves)
 };
 
 template <typename F>
-Timing time_launch(F launch, Stamp *stamp, int nblk) {
-    hipEvent_t e0, e1;
-    CHECK(hipEventCreate(&e0));
-    CHECK(hipEventCreate(&e1));
+Timing time_launch(F launch, Stamp *stamp, int nwaves) {
     launch();
     CHECK(hipDeviceSynchronize());
-    CHECK(hipEventRecord(e0));
     launch();
-    CHECK(hipEventRecord(e1));
-    CHECK(hipEventSynchronize(e1));
-    Timing t{};
-    CHECK(hipEventElapsedTime(&t.ms, e0, e1));
-    std::vector<Stamp> st(nblk);
-    CHECK(hipMemcpy(st.data(), stamp, nblk * sizeof(Stamp), hipMemcpyDeviceToHost));
+    CHECK(hipDeviceSynchronize());
+    std::vector<Stamp> st(nwaves);
+    CHECK(hipMemcpy(st.data(), stamp, nwaves * sizeof(Stamp), hipMemcpyDeviceToHost));
+    long long t0 = st[0].t0, t1 = st[0].t1;
     double cyc = 0, ticks = 0;
     for (const Stamp &s : st) {
         cyc += double(s.cycles);
-        ticks += double(s.ticks);
+        ticks += double(s.t1 - s.t0);
+        t0 = s.t0 < t0 ? s.t0 : t0;
+        t1 = s.t1 > t1 ? s.t1 : t1;
     }
+    Timing t{};
+    t.ms = double(t1 - t0) * 1e-5;
     t.ghz = ticks > 0 ? cyc / ticks * 0.1 : 0.0;
-    CHECK(hipEventDestroy(e0));
-    CHECK(hipEventDestroy(e1));
     return t;
 }
 
 // One workgroup per CU; NT / 256 waves per SIMD.  MFMA modes: TFLOP/s and the matrix
 // cores' busy fraction (MFMA count x 32 cycles over the run's cycles at its clock).
-// LDS modes: bytes and instructions per CU per cycle.
+// LDS modes: bytes and instructions per CU per cycle.  VALU modes: SIMD cycles per
+// wave64 instruction (the step's cycles over its VALU instructions, all waves of a SIMD).
 template <int MODE, int NT>
 void run_probe(const char *name, int ncu, int iters, float *sink, Stamp *stamp) {
     const Timing t = time_launch(
-        [&] { hipLaunchKernelGGL((probe_kernel<MODE, NT>), dim3(ncu), dim3(NT), 0, 0, sink, stamp, iters); }, stamp, ncu);
+        [&] { hipLaunchKernelGGL((probe_kernel<MODE, NT>), dim3(ncu), dim3(NT), 0, 0, sink, stamp, iters); }, stamp,
+        ncu * NT / 64);
     const double waves_per_cu = NT / 64.0, cycles = t.ms * 1e-3 * t.ghz * 1e9;
     if (MODE <= kMatrix64q) {
         const double mfma_per_wave = (MODE == kMatrix64q ? 64.0 : 32.0) * iters;
         const double tf = mfma_per_wave * waves_per_cu * ncu * 32768.0 / (t.ms * 1e-3) / 1e12;
         const double busy = mfma_per_wave * (waves_per_cu / 4.0) * 32.0 / cycles;
         std::printf("| %-44s | %d | %8.1f TFLOP/s | %.2f GHz | MFMA busy %.2f |\n", name, NT / 256, tf, t.ghz, busy);
+    } else if (MODE >= kExp) {
+        const double valu = (MODE == kExpFma ? 64.0 : 32.0) * iters * (waves_per_cu / 4.0);
+        const double busy = MODE == kMfmaExp ? 16.0 * iters * (waves_per_cu / 4.0) * 32.0 / cycles : 0.0;
+        std::printf("| %-44s | %d | %8.2f clk per VALU instruction | %.2f GHz | MFMA busy %.2f |\n", name, NT / 256,
+                    cycles / valu, t.ghz, busy);
     } else {
         const double instr = (MODE == kReadTr ? 32.0 : 16.0) * iters * waves_per_cu;
         const double bytes_per = MODE == kReadB128 || MODE == kWriteB128 ? 1024.0 : 512.0;
@@ -318,7 +356,7 @@ int main(int argc, char **argv) {
     float *sink;
     Stamp *stamp;
     CHECK(hipMalloc(&sink, size_t(ncu) * 1024 * sizeof(float)));
-    CHECK(hipMalloc(&stamp, size_t(ncu) * sizeof(Stamp)));
+    CHECK(hipMalloc(&stamp, size_t(ncu) * 16 * sizeof(Stamp)));
     std::printf("%d CUs, one workgroup per CU, %d steps per wave\n\n", ncu, iters);
     std::printf("| probe | waves/SIMD | rate | clock | |\n|---|---|---|---|---|\n");
     run_probe<kMfmaRegs, 256>("MFMA, register operands", ncu, iters, sink, stamp);
@@ -332,6 +370,14 @@ int main(int argc, char **argv) {
     run_probe<kReadTr, 1024>("ds_read_b64_tr_b16, 32 in flight", ncu, iters, sink, stamp);
     run_probe<kWriteB128, 1024>("ds_write_b128", ncu, iters, sink, stamp);
     run_probe<kWriteB64, 1024>("ds_write_b64", ncu, iters, sink, stamp);
+    run_probe<kExp, 512>("v_exp_f32", ncu, iters, sink, stamp);
+    run_probe<kExp, 1024>("v_exp_f32", ncu, iters, sink, stamp);
+    run_probe<kFma, 512>("v_fma_f32", ncu, iters, sink, stamp);
+    run_probe<kFma, 1024>("v_fma_f32", ncu, iters, sink, stamp);
+    run_probe<kExpFma, 512>("v_exp_f32 + v_fma_f32 interleaved", ncu, iters, sink, stamp);
+    run_probe<kExpFma, 1024>("v_exp_f32 + v_fma_f32 interleaved", ncu, iters, sink, stamp);
+    run_probe<kMfmaExp, 256>("16 MFMAs + 32 v_exp_f32, one wave", ncu, iters, sink, stamp);
+    run_probe<kMfmaExp, 512>("16 MFMAs + 32 v_exp_f32, one wave", ncu, iters, sink, stamp);
 
     const size_t bytes = size_t(1536) << 20;
     char *buf;
