@@ -68,6 +68,8 @@ enum Mode {
     kFma,           // 32 v_fma_f32 per step, 8 independent chains
     kExpFma,        // 32 v_exp_f32 and 32 v_fma_f32 per step, interleaved
     kMfmaExp,       // 16 MFMAs (register operands) and 32 v_exp_f32 per step in the same wave
+    kSplitFma,      // two waves per SIMD: one issues MFMAs (32 per step), the other v_fma_f32 (384 per step)
+    kSplitExp,      // the same with v_exp_f32 (112 per step) in the second wave
 };
 
 struct Stamp {
@@ -193,6 +195,21 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
                     if constexpr (MODE != kFma) ex[c] = __builtin_amdgcn_exp2f(-ex[c]);
                     if constexpr (MODE != kExp) fx[c] = __builtin_fmaf(fx[c], 0.999f, 0.001f);
                 }
+        } else if constexpr (MODE == kSplitFma || MODE == kSplitExp) {
+            if (wave < NT / 128) {
+#pragma unroll
+                for (int t = 0; t < 32; ++t) o[t & 3] = mfma(q[t & 7], p[t & 3], o[t & 3]);
+            } else if constexpr (MODE == kSplitFma) {
+#pragma unroll
+                for (int t = 0; t < 48; ++t)
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) fx[c] = __builtin_fmaf(fx[c], 0.999f, 0.001f);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 14; ++t)
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) ex[c] = __builtin_amdgcn_exp2f(-ex[c]);
+            }
         } else if constexpr (MODE == kMfmaExp) {
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
@@ -233,14 +250,34 @@ struct Timing {
     double ghz;  // shader clock over the loops (all waves)
 };
 
+// Loop span of the waves w with lo <= w % per_wg < hi (per_wg waves per workgroup).
+Timing span_of(const std::vector<Stamp> &st, int per_wg, int lo, int hi) {
+    long long t0 = -1, t1 = -1;
+    double cyc = 0, ticks = 0;
+    for (size_t i = 0; i < st.size(); ++i) {
+        const int w = int(i) % per_wg;
+        if (w < lo || w >= hi) continue;
+        const Stamp &s = st[i];
+        cyc += double(s.cycles);
+        ticks += double(s.t1 - s.t0);
+        t0 = t0 < 0 || s.t0 < t0 ? s.t0 : t0;
+        t1 = t1 < 0 || s.t1 > t1 ? s.t1 : t1;
+    }
+    Timing t{};
+    t.ms = double(t1 - t0) * 1e-5;
+    t.ghz = ticks > 0 ? cyc / ticks * 0.1 : 0.0;
+    return t;
+}
+
 template <typename F>
-Timing time_launch(F launch, Stamp *stamp, int nwaves) {
+Timing time_launch(F launch, Stamp *stamp, int nwaves, std::vector<Stamp> *keep = nullptr) {
     launch();
     CHECK(hipDeviceSynchronize());
     launch();
     CHECK(hipDeviceSynchronize());
     std::vector<Stamp> st(nwaves);
     CHECK(hipMemcpy(st.data(), stamp, nwaves * sizeof(Stamp), hipMemcpyDeviceToHost));
+    if (keep) *keep = st;
     long long t0 = st[0].t0, t1 = st[0].t1;
     double cyc = 0, ticks = 0;
     for (const Stamp &s : st) {
@@ -261,9 +298,20 @@ Timing time_launch(F launch, Stamp *stamp, int nwaves) {
 // wave64 instruction (the step's cycles over its VALU instructions, all waves of a SIMD).
 template <int MODE, int NT>
 void run_probe(const char *name, int ncu, int iters, float *sink, Stamp *stamp) {
+    std::vector<Stamp> st;
     const Timing t = time_launch(
         [&] { hipLaunchKernelGGL((probe_kernel<MODE, NT>), dim3(ncu), dim3(NT), 0, 0, sink, stamp, iters); }, stamp,
-        ncu * NT / 64);
+        ncu * NT / 64, &st);
+    if (MODE == kSplitFma || MODE == kSplitExp) {
+        // Waves 0..3 (one per SIMD) issue MFMAs, waves 4..7 VALU, each about 1024 cycles per step
+        // alone; each group's own loop span.  Full overlap keeps both at their lone rates.
+        const Timing tm = span_of(st, NT / 64, 0, NT / 128), tv = span_of(st, NT / 64, NT / 128, NT / 64);
+        const double mcyc = tm.ms * 1e-3 * tm.ghz * 1e9, vcyc = tv.ms * 1e-3 * tv.ghz * 1e9;
+        const double nvalu = (MODE == kSplitFma ? 384.0 : 112.0) * iters;
+        std::printf("| %-44s | 1 + 1 | MFMA busy %.2f over its loop | %.2f GHz | %.2f clk per VALU instruction |\n",
+                    name, 32.0 * iters * 32.0 / mcyc, tm.ghz, vcyc / nvalu);
+        return;
+    }
     const double waves_per_cu = NT / 64.0, cycles = t.ms * 1e-3 * t.ghz * 1e9;
     if (MODE <= kMatrix64q) {
         const double mfma_per_wave = (MODE == kMatrix64q ? 64.0 : 32.0) * iters;
@@ -378,6 +426,8 @@ int main(int argc, char **argv) {
     run_probe<kExpFma, 1024>("v_exp_f32 + v_fma_f32 interleaved", ncu, iters, sink, stamp);
     run_probe<kMfmaExp, 256>("16 MFMAs + 32 v_exp_f32, one wave", ncu, iters, sink, stamp);
     run_probe<kMfmaExp, 512>("16 MFMAs + 32 v_exp_f32, one wave", ncu, iters, sink, stamp);
+    run_probe<kSplitFma, 512>("MFMA wave beside a v_fma_f32 wave", ncu, iters, sink, stamp);
+    run_probe<kSplitExp, 512>("MFMA wave beside a v_exp_f32 wave", ncu, iters, sink, stamp);
 
     const size_t bytes = size_t(1536) << 20;
     char *buf;
