@@ -68,6 +68,8 @@ enum Mode {
     kFma,           // 32 v_fma_f32 per step, 8 independent chains
     kExpFma,        // 32 v_exp_f32 and 32 v_fma_f32 per step, interleaved
     kMfmaExp,       // 16 MFMAs (register operands) and 32 v_exp_f32 per step in the same wave
+    kMfmaFma,       // 16 MFMAs and 64 v_fma_f32 per step in the same wave (4 between MFMAs)
+    kMfmaSoft,      // 16 MFMAs, 32 v_exp_f32 and 96 v_fma_f32 per step in the same wave (a softmax's mix)
     kSplitFma,      // two waves per SIMD: one issues MFMAs (32 per step), the other v_fma_f32 (384 per step)
     kSplitExp,      // the same with v_exp_f32 (112 per step) in the second wave
 };
@@ -195,6 +197,18 @@ __global__ __launch_bounds__(NT, 1) void probe_kernel(float *sink, Stamp *stamp,
                     if constexpr (MODE != kFma) ex[c] = __builtin_amdgcn_exp2f(-ex[c]);
                     if constexpr (MODE != kExp) fx[c] = __builtin_fmaf(fx[c], 0.999f, 0.001f);
                 }
+        } else if constexpr (MODE == kMfmaFma || MODE == kMfmaSoft) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                o[t & 3] = mfma(q[t & 7], p[t & 3], o[t & 3]);
+#pragma unroll
+                for (int u = 0; u < (MODE == kMfmaFma ? 4 : 6); ++u)
+                    fx[(4 * t + u) & 7] = __builtin_fmaf(fx[(4 * t + u) & 7], 0.999f, 0.001f);
+                if constexpr (MODE == kMfmaSoft) {
+                    ex[(2 * t) & 7] = __builtin_amdgcn_exp2f(-ex[(2 * t) & 7]);
+                    ex[(2 * t + 1) & 7] = __builtin_amdgcn_exp2f(-ex[(2 * t + 1) & 7]);
+                }
+            }
         } else if constexpr (MODE == kSplitFma || MODE == kSplitExp) {
             if (wave < NT / 128) {
 #pragma unroll
@@ -319,8 +333,10 @@ void run_probe(const char *name, int ncu, int iters, float *sink, Stamp *stamp) 
         const double busy = mfma_per_wave * (waves_per_cu / 4.0) * 32.0 / cycles;
         std::printf("| %-44s | %d | %8.1f TFLOP/s | %.2f GHz | MFMA busy %.2f |\n", name, NT / 256, tf, t.ghz, busy);
     } else if (MODE >= kExp) {
-        const double valu = (MODE == kExpFma ? 64.0 : 32.0) * iters * (waves_per_cu / 4.0);
-        const double busy = MODE == kMfmaExp ? 16.0 * iters * (waves_per_cu / 4.0) * 32.0 / cycles : 0.0;
+        const double per = MODE == kExpFma || MODE == kMfmaFma ? 64.0 : MODE == kMfmaSoft ? 128.0 : 32.0;
+        const double valu = per * iters * (waves_per_cu / 4.0);
+        const bool mf = MODE == kMfmaExp || MODE == kMfmaFma || MODE == kMfmaSoft;
+        const double busy = mf ? 16.0 * iters * (waves_per_cu / 4.0) * 32.0 / cycles : 0.0;
         std::printf("| %-44s | %d | %8.2f clk per VALU instruction | %.2f GHz | MFMA busy %.2f |\n", name, NT / 256,
                     cycles / valu, t.ghz, busy);
     } else {
@@ -426,6 +442,9 @@ int main(int argc, char **argv) {
     run_probe<kExpFma, 1024>("v_exp_f32 + v_fma_f32 interleaved", ncu, iters, sink, stamp);
     run_probe<kMfmaExp, 256>("16 MFMAs + 32 v_exp_f32, one wave", ncu, iters, sink, stamp);
     run_probe<kMfmaExp, 512>("16 MFMAs + 32 v_exp_f32, one wave", ncu, iters, sink, stamp);
+    run_probe<kMfmaFma, 256>("16 MFMAs + 64 v_fma_f32, one wave", ncu, iters, sink, stamp);
+    run_probe<kMfmaSoft, 256>("16 MFMAs + 32 exp + 96 fma, one wave", ncu, iters, sink, stamp);
+    run_probe<kMfmaSoft, 512>("16 MFMAs + 32 exp + 96 fma, one wave", ncu, iters, sink, stamp);
     run_probe<kSplitFma, 512>("MFMA wave beside a v_fma_f32 wave", ncu, iters, sink, stamp);
     run_probe<kSplitExp, 512>("MFMA wave beside a v_exp_f32 wave", ncu, iters, sink, stamp);
 
