@@ -400,12 +400,9 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     };
     load_rows(ks_lds, kp, a.k.row_stride);
     load_rows(vs_lds, vp, a.v.row_stride);
-    wait_vmem();  // only the tile copies are in flight inside the loop
-    __syncthreads();
-    // The wave's K rows stay in registers as the S B operands for the whole kernel.
+    // The wave's K rows stay in registers as the S B operands for the whole kernel
+    // (read from LDS once the rows have landed, before the block loop).
     f16x8 kreg[HD / 16];
-#pragma unroll
-    for (int g = 0; g < HD / 16; ++g) kreg[g] = rd0.a_operand(ks_lds, 32 * kg, g);
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) {
@@ -575,7 +572,19 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     const int i1 = CAUSAL ? clampi(first_at(kw0 - 31 - causal_off), 0, n_qb) : 0;
     const int i2 = CAUSAL ? clampi(first_at(kw0 + 31 - causal_off), i1, n_qb) : 0;
     const int i3 = clampi(first_at(sq - 31), i2, n_qb);
+    // The first Q / dO copies go out before the K / V rows are waited for, so
+    // the two latencies overlap: the wait leaves this wave's copies of the
+    // first block in flight (Q and dO, and the LSE / D row for waves 0 and 1).
     if (n_qb > 0) issue_next(0);
+    if (n_qb > 0 && wave < 2)
+        wait_vmem_n<2 * (BM * (HD / 8) / NT) + 1>();
+    else if (n_qb > 0)
+        wait_vmem_n<2 * (BM * (HD / 8) / NT)>();
+    else
+        wait_vmem();
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < HD / 16; ++g) kreg[g] = rd0.a_operand(ks_lds, 32 * kg, g);
     for (int hidx = 0; hidx < G && n_qb > 0; ++hidx) {
         for (int i = 0; i < i1; ++i) step(i, std::true_type{}, false);
         for (int i = i1; i < i2; ++i) step(i, std::true_type{}, true);
@@ -583,21 +592,25 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
         for (int i = i3; i < n_qb; ++i) step(i, std::true_type{}, true);
     }
 
-    // Partial sums: half 1 hands over its dK, half 0 its dV (lane-contiguous
-    // fp32, conflict-free), then half 0 finishes dK and half 1 dV.
+    // Partial sums: half 1 hands over its dK, half 0 its dV, then half 0
+    // finishes dK and half 1 dV.  Chunk-major fp32: chunk c (accumulator rows
+    // 4c..4c+3 of tile dt) of every lane is one 1 KB run per wave, one
+    // conflict-free ds_write_b128 / ds_read_b128 each.
     __syncthreads();  // every wave is done with the tiles
     float *xk = reinterpret_cast<float *>(smem) + kg * (HD / 32) * 16 * 64;
     float *xv = xk + 4 * (HD / 32) * 16 * 64;
-    if (half) {
+    {
+        float *xout = half ? xk : xv;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) xk[(dt * 16 + r) * 64 + lane] = dk[dt][r];
-    } else {
+            for (int a4 = 0; a4 < 4; ++a4) {
+                const f32x16 &src = half ? dk[dt] : dv[dt];
+                f32x4 v;
 #pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) xv[(dt * 16 + r) * 64 + lane] = dv[dt][r];
+                for (int t = 0; t < 4; ++t) v[t] = src[4 * a4 + t];
+                *reinterpret_cast<f32x4 *>(xout + ((dt * 4 + a4) * 64 + lane) * 4) = v;
+            }
     }
     __syncthreads();
     if (!kv_ok) return;
@@ -610,11 +623,12 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
             f16x4 o4;
+            const f32x4 x4 = *reinterpret_cast<const f32x4 *>(xin + ((dt * 4 + a4) * 64 + lane) * 4);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int r = 4 * a4 + t;
                 const float mine = half ? dv[dt][r] : dk[dt][r];
-                o4[t] = (f16)((mine + xin[(dt * 16 + r) * 64 + lane]) * oscale);
+                o4[t] = (f16)((mine + x4[t]) * oscale);
             }
             *reinterpret_cast<f16x4 *>(orow + dt * 32 + 8 * a4 + 4 * hh) = o4;
         }
