@@ -107,6 +107,9 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
 // explicitly (wait_vmem / wait_vmem_n) before a barrier that publishes the
 // tile, and issue no other vector-memory loads while copies are in flight
 // (the compiler's own waits for those would then also cover the copies).
+// An SALU write of M0 needs one wait state before an LDS-DMA load reads it
+// (the CDNA manually-inserted wait states; the compiler inserts none inside
+// inline assembly), hence the s_nop after each M0 write below.
 __device__ __forceinline__ void g2l16(const void *g, char *lds_base) {
     const uint32_t l =
         __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds_base);
@@ -114,6 +117,7 @@ __device__ __forceinline__ void g2l16(const void *g, char *lds_base) {
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, off\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -134,6 +138,7 @@ __device__ __forceinline__ void g2l16_batch(const void *const (&g)[N], const uin
         asm volatile(
             "s_mov_b32 %0, m0\n\t"
             "s_mov_b32 m0, %2\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %1, off\n\t"
             "s_mov_b32 m0, %0"
             : "=&s"(saved)
@@ -143,8 +148,10 @@ __device__ __forceinline__ void g2l16_batch(const void *const (&g)[N], const uin
         asm volatile(
             "s_mov_b32 %0, m0\n\t"
             "s_mov_b32 m0, %3\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %1, off\n\t"
             "s_mov_b32 m0, %4\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %2, off\n\t"
             "s_mov_b32 m0, %0"
             : "=&s"(saved)
@@ -155,12 +162,16 @@ __device__ __forceinline__ void g2l16_batch(const void *const (&g)[N], const uin
         asm volatile(
             "s_mov_b32 %0, m0\n\t"
             "s_mov_b32 m0, %5\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %1, off\n\t"
             "s_mov_b32 m0, %6\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %2, off\n\t"
             "s_mov_b32 m0, %7\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %3, off\n\t"
             "s_mov_b32 m0, %8\n\t"
+            "s_nop 0\n\t"
             "global_load_lds_dwordx4 %4, off\n\t"
             "s_mov_b32 m0, %0"
             : "=&s"(saved)
@@ -174,6 +185,7 @@ __device__ __forceinline__ void g2l4_to(const void *g, uint32_t l) {
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dword %1, off\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
