@@ -280,30 +280,32 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV kernel: 8 waves over 128 keys of one (batch, KV head).  Wave w owns
-// keys 32 (w % 4) .. +31 and, of every 64-query block, the 32-query half
-// w / 4, so two waves share each SIMD and the register file holds one 32 x 32
-// S / dP tile per wave next to its dK/dV accumulators.  K and V stay in LDS
-// for the whole kernel as MFMA B operands.  For every q-head of the GQA group
-// and every query block that sees these keys, Q, dO, LSE and D are copied
-// HBM -> LDS (two stages); S = Q K^T and dP = dO V^T read Q, dO as natural A
-// operands, dV^T += dO^T P and dK^T += Q^T dS read them transposed.  The
-// group's contributions accumulate in fp32 registers (no per-q-head dK/dV
-// buffers); at the end the two waves of a key range add their partial sums
-// through LDS, one wave finishing dK and the other dV.  Needs D and
-// LSE*log2(e) (the dsum workspace) from the dQ or the preprocess kernel.
-constexpr int kDkvThreads = 512;
+// dK/dV kernel: 4 waves over 128 keys of one (batch, KV head), two workgroups
+// per CU.  Wave w owns keys 32 w .. +31 and every query of every 32-query
+// block, so the register file holds one 32 x 32 S / dP tile per wave next to
+// its dK/dV accumulators, and each SIMD runs one wave of each of two
+// independent workgroups: one workgroup's block barriers, prologue and
+// epilogue overlap the other's blocks.  K goes HBM -> registers as the S B
+// operands; V stays in LDS for the whole kernel as the dP B operands.  For
+// every q-head of the GQA group and every query block that sees these keys,
+// Q, dO, LSE and D are copied HBM -> LDS (two stages); S = Q K^T and
+// dP = dO V^T read Q, dO as natural A operands, dV^T += dO^T P and
+// dK^T += Q^T dS read them transposed.  The group's contributions accumulate
+// in fp32 registers (no per-q-head dK/dV buffers) and each wave stores its
+// keys' rows.  Needs D and LSE*log2(e) (the dsum workspace) from the dQ or
+// the preprocess kernel.
+constexpr int kDkvThreads = 256;
 
 template <int HD>
 struct DkvCfg {
     static constexpr int BN = 128, NT = kDkvThreads;
-    static constexpr int BM = 64;                         // queries per block (one 32-query half per wave)
-    static constexpr int QTILE = BM * HD * 2;             // Q or dO tile, natural layout
-    static constexpr int STAGE = 2 * QTILE + 2 * BM * 4;  // Q, dO, LSE, D
-    static constexpr int KTILE = BN * HD * 2;             // the workgroup's K (or V) rows
-    static constexpr int LDS = 2 * STAGE + 2 * KTILE;
-    static constexpr int XCH = 2 * BN * HD * 4;           // dK and dV partials handed between waves
-    static_assert(XCH <= LDS, "partial-sum exchange reuses the tiles' LDS");
+    static constexpr int BM = 32;                             // queries per block
+    static constexpr int QTILE = BM * HD * 2;                 // Q or dO tile, natural layout
+    static constexpr int LROWS = 64;                          // LSE / D slots: one 4-byte DMA per lane
+    static constexpr int STAGE = 2 * QTILE + 2 * LROWS * 4;   // Q, dO, LSE, D
+    static constexpr int VTILE = BN * HD * 2;                 // the workgroup's V rows
+    static constexpr int LDS = 2 * STAGE + VTILE;
+    static_assert(2 * LDS <= 160 * 1024, "two workgroups per CU");
 };
 
 // Varlen work orders (order_items in fa_common.h).  dK/dV: item it = b * nnb
@@ -339,14 +341,14 @@ __global__ __launch_bounds__(kOrderThreads) void dq_order_kernel(const fa_bwd_ar
 }
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_args a, const int nnb) {
+__global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_args a, const int nnb) {
     using C = DkvCfg<HD>;
-    constexpr int BN = C::BN, BM = C::BM, NT = C::NT;
+    constexpr int BN = C::BN, BM = C::BM, NT = C::NT, LROWS = C::LROWS;
     __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-    const int kg = wave & 3, half = wave >> 2;                  // key group, query half
+    const int kg = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave's key group (wave-uniform)
+    const int wave = kg;
     const int col = lane & 31, hh = lane >> 5;
     int b, hk, nb;
     if (a.work_order && a.cu_seqlens_k) {
@@ -381,12 +383,11 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     const bool kv_ok = key < sk;
     TileReader<HD> rd0;
     rd0.init(lane);
-    // K, V rows of the workgroup as MFMA B operands (lane: key col,
+    // V rows of the workgroup as MFMA B operands (lane: key col,
     // d = 16g + 8hh + 0..7).  Row r of each 32-row group is stored at position
     // sigma(r), so the B-operand read of key col is the conflict-free A-operand
     // pattern.
-    char *ks_lds = smem + 2 * C::STAGE;
-    char *vs_lds = ks_lds + C::KTILE;
+    char *vs_lds = smem + 2 * C::STAGE;
     auto load_rows = [&](char *tile, const f16 *src, int64_t rs) {
         constexpr int KCH = HD / 8;
 #pragma unroll
@@ -398,11 +399,17 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
             g2l16(src + r * rs + 8 * (cs ^ swz<KCH>(pos)), tile + base * 16);
         }
     };
-    load_rows(ks_lds, kp, a.k.row_stride);
     load_rows(vs_lds, vp, a.v.row_stride);
-    // The wave's K rows stay in registers as the S B operands for the whole kernel
-    // (read from LDS once the rows have landed, before the block loop).
+    // The wave's K rows stay in registers as the S B operands for the whole
+    // kernel, loaded straight from HBM (lane: key col, d = 16g + 8hh + 0..7;
+    // keys past the sequence re-read its last row, their columns never stored).
+    // Issued after the V copies and waited for with them at the first block.
     f16x8 kreg[HD / 16];
+    {
+        const f16 *kr = kp + int64_t(min(key, sk - 1)) * a.k.row_stride + 8 * hh;
+#pragma unroll
+        for (int g = 0; g < HD / 16; ++g) kreg[g] = *reinterpret_cast<const f16x8 *>(kr + 16 * g);
+    }
     f32x16 dk[HD / 32], dv[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) {
@@ -441,10 +448,11 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
             dma_tile<HD, BM, NT>(qt, nq, qrs, q0, sq - 1, wave, lane);
             dma_tile<HD, BM, NT>(qt + C::QTILE, ndo, dors, q0, sq - 1, wave, lane);
         }
-        // LSE*log2(e) (second plane of the dsum workspace) and D per query row.
+        // LSE*log2(e) (second plane of the dsum workspace) and D per query row
+        // (64 lanes each; the block reads the first BM).
         const int r = min(q0 + lane, sq - 1);
         if (wave == 0) g2l4_to(nd + lse_plane + r, lf_l);
-        if (wave == 1) g2l4_to(nd + r, lf_l + BM * 4);
+        if (wave == 1) g2l4_to(nd + r, lf_l + LROWS * 4);
         nq_row += q_step;
         ndo_row += do_step;
         if (++ni == n_qb) {
@@ -458,14 +466,14 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
         }
     };
 
-    // The wave's 32-query half of block j: S = Q K^T and dP = dO V^T, P, dS,
-    // then dV^T += dO^T P and dK^T += Q^T dS.
+    // Block j (queries qh0 ..): S = Q K^T and dP = dO V^T, P, dS, then
+    // dV^T += dO^T P and dK^T += Q^T dS.
     auto block = [&](int j, int qh0, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const char *qt = smem + (j & 1) * C::STAGE;
         const char *ot = qt + C::QTILE;
         const float *lf = reinterpret_cast<const float *>(ot + C::QTILE);
-        const int r0 = 32 * half;
+        constexpr int r0 = 0;
         // The per-read LDS addresses are recomputed here from an opaque copy of
         // the lane's base offsets: hoisted out of the loop they would hold
         // dozens of registers for the whole kernel.
@@ -491,8 +499,8 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
 #pragma unroll
         for (int r8 = 0; r8 < 2; ++r8) {
             const int ql0 = r0 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
-            const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + BM + ql0);
-            const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + BM + ql0 + 4);
+            const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + LROWS + ql0);
+            const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + LROWS + ql0 + 4);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 dp[8 * r8 + u] = d_a[u];
@@ -552,7 +560,7 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
     };
 
     // Each wave walks the same sequence of blocks (one barrier per block) in
-    // four straight loops per q-head: blocks whose half sees none of its keys
+    // four straight loops per q-head: blocks that see none of the wave's keys
     // (skipped), diagonal blocks (masked), full blocks, and a ragged last
     // block (masked).  Straight loops keep the dK/dV accumulators in place;
     // branching per block would copy them at every join.  Keys past the
@@ -562,29 +570,23 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
         wait_vmem();
         __syncthreads();  // block j is in LDS; every wave is done with stage (j & 1) ^ 1
         if (nh < G) issue_next((j & 1) ^ 1);
-        if (compute) block(j, (m_first + i) * BM + 32 * half, mask_tag);
+        if (compute) block(j, (m_first + i) * BM, mask_tag);
         ++j;
     };
     auto clampi = [](int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); };
-    // Smallest block index i whose half start (m_first + i) * BM + 32 * half reaches x.
-    auto first_at = [&](int x) { return ((x - 32 * half + BM - 1) >> 6) - m_first; };
-    static_assert(BM == 64, "first_at divides by 64");
+    // Smallest block index i whose start (m_first + i) * BM reaches x.
+    auto first_at = [&](int x) { return ((x + BM - 1) >> 5) - m_first; };
+    static_assert(BM == 32, "first_at divides by 32");
     const int i1 = CAUSAL ? clampi(first_at(kw0 - 31 - causal_off), 0, n_qb) : 0;
     const int i2 = CAUSAL ? clampi(first_at(kw0 + 31 - causal_off), i1, n_qb) : 0;
     const int i3 = clampi(first_at(sq - 31), i2, n_qb);
-    // The first Q / dO copies go out before the K / V rows are waited for, so
-    // the two latencies overlap: the wait leaves this wave's copies of the
-    // first block in flight (Q and dO, and the LSE / D row for waves 0 and 1).
-    if (n_qb > 0) issue_next(0);
-    if (n_qb > 0 && wave < 2)
-        wait_vmem_n<2 * (BM * (HD / 8) / NT) + 1>();
-    else if (n_qb > 0)
-        wait_vmem_n<2 * (BM * (HD / 8) / NT)>();
+    // The first block's copies go out with the V rows and the K loads; the
+    // first step's wait and barrier cover all of them.  With no block to walk,
+    // the V copies still land before the wave ends.
+    if (n_qb > 0)
+        issue_next(0);
     else
         wait_vmem();
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < HD / 16; ++g) kreg[g] = rd0.a_operand(ks_lds, 32 * kg, g);
     for (int hidx = 0; hidx < G && n_qb > 0; ++hidx) {
         for (int i = 0; i < i1; ++i) step(i, std::true_type{}, false);
         for (int i = i1; i < i2; ++i) step(i, std::true_type{}, true);
@@ -592,45 +594,23 @@ __global__ __launch_bounds__(kDkvThreads, 1) void bwd_dkdv_kernel(const fa_bwd_a
         for (int i = i3; i < n_qb; ++i) step(i, std::true_type{}, true);
     }
 
-    // Partial sums: half 1 hands over its dK, half 0 its dV, then half 0
-    // finishes dK and half 1 dV.  Chunk-major fp32: chunk c (accumulator rows
-    // 4c..4c+3 of tile dt) of every lane is one 1 KB run per wave, one
-    // conflict-free ds_write_b128 / ds_read_b128 each.
-    __syncthreads();  // every wave is done with the tiles
-    float *xk = reinterpret_cast<float *>(smem) + kg * (HD / 32) * 16 * 64;
-    float *xv = xk + 4 * (HD / 32) * 16 * 64;
-    {
-        float *xout = half ? xk : xv;
-#pragma unroll
-        for (int dt = 0; dt < HD / 32; ++dt)
-#pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                const f32x16 &src = half ? dk[dt] : dv[dt];
-                f32x4 v;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) v[t] = src[4 * a4 + t];
-                *reinterpret_cast<f32x4 *>(xout + ((dt * 4 + a4) * 64 + lane) * 4) = v;
-            }
-    }
-    __syncthreads();
+    // Lane (col, hh) holds d = 32 dt + 8 a4 + 4 hh + t (accumulator 4 a4 + t)
+    // of key `key`: four consecutive fp16 per store.
     if (!kv_ok) return;
-    const fa_tensor &out_t = half ? a.dv : a.dk;
-    f16 *orow = (f16 *)out_t.ptr + base_off(out_t, packed_k, b, si.k_start, hk) + int64_t(key) * out_t.row_stride;
-    const float *xin = half ? xv : xk;
-    const float oscale = half ? 1.f : a.softmax_scale;
+    f16 *dkrow = (f16 *)a.dk.ptr + base_off(a.dk, packed_k, b, si.k_start, hk) + int64_t(key) * a.dk.row_stride;
+    f16 *dvrow = (f16 *)a.dv.ptr + base_off(a.dv, packed_k, b, si.k_start, hk) + int64_t(key) * a.dv.row_stride;
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt)
 #pragma unroll
         for (int a4 = 0; a4 < 4; ++a4) {
-            f16x4 o4;
-            const f32x4 x4 = *reinterpret_cast<const f32x4 *>(xin + ((dt * 4 + a4) * 64 + lane) * 4);
+            f16x4 k4, v4;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const int r = 4 * a4 + t;
-                const float mine = half ? dv[dt][r] : dk[dt][r];
-                o4[t] = (f16)((mine + x4[t]) * oscale);
+                k4[t] = (f16)(dk[dt][4 * a4 + t] * a.softmax_scale);
+                v4[t] = (f16)dv[dt][4 * a4 + t];
             }
-            *reinterpret_cast<f16x4 *>(orow + dt * 32 + 8 * a4 + 4 * hh) = o4;
+            *reinterpret_cast<f16x4 *>(dkrow + dt * 32 + 8 * a4 + 4 * hh) = k4;
+            *reinterpret_cast<f16x4 *>(dvrow + dt * 32 + 8 * a4 + 4 * hh) = v4;
         }
 }
 
