@@ -196,15 +196,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         const int n0 = nb * BN;
         if (CAUSAL && MASK && n0 > q_lo + 31 + causal_off) return;  // no visible key for this wave
         if (q_lo >= sq) return;                                      // no query row of the sequence
-        const char *ks = smem + buf * C::STAGE;
-        const char *vs = ks + C::TILE;
         // Operand reads run kDqPipe - 1 MFMA steps ahead through a ring of
         // registers, with a scheduling fence per step, so an MFMA does not
-        // wait for the LDS read issued just before it.  The per-read
-        // addresses are recomputed from an opaque copy of the lane's bases
-        // (hoisted, they would hold registers for the whole kernel).
-        TileReader<HD> r = rd;
-        asm volatile("" : "+v"(r.a_base), "+v"(r.tr_base[0]), "+v"(r.tr_base[1]));
+        // wait for the LDS read issued just before it.  The lane's read bases
+        // get this block's stage added once (opaque, so the per-read
+        // addresses are not hoisted to hold registers for the whole kernel);
+        // each read is then one XOR and an immediate (TileReader::a_operand_at).
+        const int soff = buf * C::STAGE;
+        static_assert(C::STAGE % 512 == 0, "stage offsets must be multiples of 512 bytes");
+        int ab = rd.a_base + soff, tb0 = rd.tr_base[0] + soff, tb1 = rd.tr_base[1] + soff;
+        asm volatile("" : "+v"(ab), "+v"(tb0), "+v"(tb1));
         f16x8 opnd[kDqPipe];
         // S / dP step t: chain c = t % 4 (s[0], dp[0], s[1], dp[1]) at K step
         // g = t / 4, so consecutive MFMAs feed four independent accumulators
@@ -212,10 +213,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         constexpr int NSD = 4 * (HD / 16), NDQ = 4 * (HD / 32), NDT = HD / 32;
         auto read_sd = [&](int t) FA_INLINE {
             const int c = t & 3;
-            opnd[t % kDqPipe] = r.a_operand((c & 1) ? vs : ks, 32 * (c >> 1), t >> 2);
+            opnd[t % kDqPipe] = rd.a_operand_at(smem + (c & 1) * C::TILE + 32 * (c >> 1) * (HD * 2), ab, t >> 2);
         };
         // dQ step u: accumulator dt = u % NDT at key step gg = u / NDT.
-        auto read_dq = [&](int u) FA_INLINE { opnd[u % kDqPipe] = r.tr_operand(ks, 16 * (u / NDT), u % NDT); };
+        auto read_dq = [&](int u) FA_INLINE {
+            opnd[u % kDqPipe] = rd.tr_operand_at(smem + 16 * (u / NDT) * (HD * 2), tb0, tb1, u % NDT);
+        };
         f32x16 s[2], dp[2];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -466,19 +469,26 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         }
     };
 
+    // The wave's V rows as a read base: the lane's A-operand base plus the rows'
+    // LDS offset.  Every tile offset added to a lane base is a multiple of 512
+    // bytes (TileReader::a_operand_at).
+    const int vb0 = rd0.a_base + 2 * C::STAGE + 32 * kg * (HD * 2);
+    static_assert(C::STAGE % 512 == 0 && C::QTILE % 512 == 0 && (32 * HD * 2) % 512 == 0,
+                  "tile offsets must be multiples of 512 bytes");
+
     // Block j (queries qh0 ..): S = Q K^T and dP = dO V^T, P, dS, then
     // dV^T += dO^T P and dK^T += Q^T dS.
     auto block = [&](int j, int qh0, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const char *qt = smem + (j & 1) * C::STAGE;
-        const char *ot = qt + C::QTILE;
-        const float *lf = reinterpret_cast<const float *>(ot + C::QTILE);
-        constexpr int r0 = 0;
-        // The per-read LDS addresses are recomputed here from an opaque copy of
-        // the lane's base offsets: hoisted out of the loop they would hold
-        // dozens of registers for the whole kernel.
-        TileReader<HD> rd = rd0;
-        asm volatile("" : "+v"(rd.a_base), "+v"(rd.tr_base[0]), "+v"(rd.tr_base[1]));
+        const int soff = (j & 1) * C::STAGE;
+        const float *lf = reinterpret_cast<const float *>(smem + soff + 2 * C::QTILE);
+        // The lane's read bases with this block's stage added (once per block:
+        // opaque, so the per-read addresses are not hoisted out of the loop,
+        // where they would hold dozens of registers for the whole kernel); each
+        // read is then one XOR (TileReader::a_operand_at / tr_operand_at) and
+        // an immediate: Q at 0, dO at QTILE, rows 16.. of a tile at 16 rows.
+        int qb = rd0.a_base + soff, tb0 = rd0.tr_base[0] + soff, tb1 = rd0.tr_base[1] + soff, vb = vb0;
+        asm volatile("" : "+v"(qb), "+v"(tb0), "+v"(tb1), "+v"(vb));
         // Operand reads run PIPE steps ahead of the MFMAs that use them, and a
         // scheduling fence after each step keeps that order, so the dK/dV
         // accumulators, the S/dP tiles and the operands in flight fit the
@@ -486,9 +496,9 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         constexpr int PIPE = 2, NG = HD / 16;
         f16x8 qa[PIPE], oa[PIPE], va[PIPE];
         auto ld = [&](int g) {
-            qa[g % PIPE] = rd.a_operand(qt, r0, g);
-            oa[g % PIPE] = rd.a_operand(ot, r0, g);
-            va[g % PIPE] = rd.a_operand(vs_lds, 32 * kg, g);
+            qa[g % PIPE] = rd0.a_operand_at(smem, qb, g);
+            oa[g % PIPE] = rd0.a_operand_at(smem + C::QTILE, qb, g);
+            va[g % PIPE] = rd0.a_operand_at(smem, vb, g);
         };
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -498,7 +508,7 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         f32x16 s = zero16(), dp;
 #pragma unroll
         for (int r8 = 0; r8 < 2; ++r8) {
-            const int ql0 = r0 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
+            const int ql0 = 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
             const f32x4 d_a = *reinterpret_cast<const f32x4 *>(lf + LROWS + ql0);
             const f32x4 d_b = *reinterpret_cast<const f32x4 *>(lf + LROWS + ql0 + 4);
 #pragma unroll
@@ -516,7 +526,7 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         }
 #pragma unroll
         for (int r8 = 0; r8 < 2; ++r8) {
-            const int ql0 = r0 + 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
+            const int ql0 = 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
             const f32x4 l_a = *reinterpret_cast<const f32x4 *>(lf + ql0);
             const f32x4 l_b = *reinterpret_cast<const f32x4 *>(lf + ql0 + 4);
 #pragma unroll
@@ -545,8 +555,8 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         constexpr int NT2 = 2 * (HD / 32);
         f16x8 ta[PIPE], tq[PIPE];
         auto ldt = [&](int t) {
-            ta[t % PIPE] = rd.tr_operand(ot, r0 + 16 * (t & 1), t >> 1);
-            tq[t % PIPE] = rd.tr_operand(qt, r0 + 16 * (t & 1), t >> 1);
+            ta[t % PIPE] = rd0.tr_operand_at(smem + C::QTILE + 16 * (t & 1) * (HD * 2), tb0, tb1, t >> 1);
+            tq[t % PIPE] = rd0.tr_operand_at(smem + 16 * (t & 1) * (HD * 2), tb0, tb1, t >> 1);
         };
 #pragma unroll
         for (int t = 0; t < PIPE - 1; ++t) ldt(t);

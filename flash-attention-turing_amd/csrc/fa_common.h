@@ -323,6 +323,19 @@ struct TileReader {
         const f16x4 hi = lds_tr4(t, tr_base[1] ^ (dt << 6));
         return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
+    // The same reads from lane bases that already include a tile offset t, a
+    // multiple of 512 bytes: the step XOR (g << 5, dt << 6: bits 5-7) and the
+    // add of t (bits 9 and up, no carry out of the low bits) commute, so
+    // (base + t) ^ m == (base ^ m) + t.  A caller forms base + t once per tile
+    // and each read is then one XOR, the rest of the address an immediate.
+    __device__ __forceinline__ f16x8 a_operand_at(const char *lds0, int base_t, int g) const {
+        return lds_ld16(lds0, base_t ^ (g << 5));
+    }
+    __device__ __forceinline__ f16x8 tr_operand_at(const char *lds0, int b0_t, int b1_t, int dt) const {
+        const f16x4 lo = lds_tr4(lds0, b0_t ^ (dt << 6));
+        const f16x4 hi = lds_tr4(lds0, b1_t ^ (dt << 6));
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
 };
 
 // ---------------------------------------------------------------------------

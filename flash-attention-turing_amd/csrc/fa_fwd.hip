@@ -354,14 +354,20 @@ __global__ __launch_bounds__(256, QT == 2 || HD == 128 ? 2 : 3) void fwd_kernel(
         } else {
             // Each operand feeds both tiles' MFMAs.  The reads run PIPE steps
             // ahead behind scheduling fences (all of them hoisted to the top
-            // would not fit the registers of two waves per SIMD), from an opaque
-            // copy of the lane's base offsets (hoisted out of the loop, the
-            // per-read addresses would hold registers for the whole kernel).
+            // would not fit the registers of two waves per SIMD), from the
+            // lane's base offsets with this block's stage added once (opaque:
+            // hoisted out of the loop, the per-read addresses would hold
+            // registers for the whole kernel); each read is one XOR and an
+            // immediate (TileReader::a_operand_at).
             constexpr int PIPE = 3, NS = 2 * (HD / 16), NPV = 4 * (HD / 32);
-            TileReader<HD> r = rd;
-            asm volatile("" : "+v"(r.a_base), "+v"(r.tr_base[0]), "+v"(r.tr_base[1]));
+            const int soff = buf * C::STAGE;
+            static_assert(C::STAGE % 512 == 0, "stage offsets must be multiples of 512 bytes");
+            int ab = rd.a_base + soff, tb0 = rd.tr_base[0] + soff, tb1 = rd.tr_base[1] + soff;
+            asm volatile("" : "+v"(ab), "+v"(tb0), "+v"(tb1));
             f16x8 op[PIPE];
-            auto rd_k = [&](int u) FA_INLINE { op[u % PIPE] = r.a_operand(ks, 32 * (u / (HD / 16)), u % (HD / 16)); };
+            auto rd_k = [&](int u) FA_INLINE {
+                op[u % PIPE] = rd.a_operand_at(smem + 32 * (u / (HD / 16)) * (HD * 2), ab, u % (HD / 16));
+            };
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < PIPE - 1; ++u) rd_k(u);
@@ -374,7 +380,9 @@ __global__ __launch_bounds__(256, QT == 2 || HD == 128 ? 2 : 3) void fwd_kernel(
                 __builtin_amdgcn_sched_barrier(0);
             }
             softmax();
-            auto rd_v = [&](int u) FA_INLINE { op[u % PIPE] = r.tr_operand(vs, 16 * (u & 3), u >> 2); };
+            auto rd_v = [&](int u) FA_INLINE {
+                op[u % PIPE] = rd.tr_operand_at(smem + C::TILE + 16 * (u & 3) * (HD * 2), tb0, tb1, u >> 2);
+            };
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < PIPE - 1; ++u) rd_v(u);
@@ -456,19 +464,21 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const fa_fwd_args a, con
     auto matrix = [&](int j, auto pv_tag, auto s_tag) FA_INLINE {
         constexpr bool DO_PV = decltype(pv_tag)::value, DO_S = decltype(s_tag)::value;
         constexpr int T0 = DO_PV ? 0 : NPV, T1 = DO_S ? NPV + NS : NPV;
-        const char *ks = smem + (j & 1) * C::STAGE;
-        const char *vs = ks + C::TILE;
-        // The per-read LDS addresses are recomputed from an opaque copy of the
-        // lane's base offsets: hoisted out of the loop they would hold
-        // registers for the whole kernel.
-        TileReader<HD> r = rd;
-        asm volatile("" : "+v"(r.a_base), "+v"(r.tr_base[0]), "+v"(r.tr_base[1]));
+        // The lane's read bases with stage j & 1 added once (opaque: hoisted out
+        // of the loop, the per-read addresses would hold registers for the
+        // whole kernel); each read is then one XOR and an immediate
+        // (TileReader::a_operand_at).
+        const int soff = (j & 1) * C::STAGE;
+        static_assert(C::STAGE % 512 == 0, "stage offsets must be multiples of 512 bytes");
+        int ab = rd.a_base + soff, tb0 = rd.tr_base[0] + soff, tb1 = rd.tr_base[1] + soff;
+        asm volatile("" : "+v"(ab), "+v"(tb0), "+v"(tb1));
         f16x8 opnd[kPpPipe];
         auto read = [&](int t) FA_INLINE {
             if (t < NPV)
-                opnd[t % kPpPipe] = r.tr_operand(vs, 16 * (t & 3), t >> 2);
+                opnd[t % kPpPipe] = rd.tr_operand_at(smem + C::TILE + 16 * (t & 3) * (HD * 2), tb0, tb1, t >> 2);
             else
-                opnd[t % kPpPipe] = r.a_operand(ks, 32 * ((t - NPV) / (HD / 16)), (t - NPV) % (HD / 16));
+                opnd[t % kPpPipe] =
+                    rd.a_operand_at(smem + 32 * ((t - NPV) / (HD / 16)) * (HD * 2), ab, (t - NPV) % (HD / 16));
         };
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
