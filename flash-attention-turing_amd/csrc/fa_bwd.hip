@@ -175,9 +175,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
     f32x16 dq[HD / 32];
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) dq[i] = zero16();
-    // At head_dim 64 (bound by VALU work) the dP^T accumulators start from -D,
-    // so dP - D comes out of the MFMAs; at 128 the 16 registers of that seed
-    // do not fit and D is subtracted per element.
+    // The dP^T accumulators start from -D (one value per lane: the lane's
+    // query), so dP - D comes out of the MFMAs.  At head_dim 64 the seed tile
+    // is held for the whole kernel; at 128 its 16 registers do not fit there,
+    // so each block fills it just before its dP chains (16 moves instead of
+    // 32 subtractions).
     f32x16 dp_init = zero16();
     if constexpr (HD == 64) {
 #pragma unroll
@@ -220,6 +222,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
             opnd[u % kDqPipe] = rd.tr_operand_at(smem + 16 * (u / NDT) * (HD * 2), tb0, tb1, u % NDT);
         };
         f32x16 s[2], dp[2];
+        f32x16 seed = dp_init;
+        if constexpr (HD == 128) {
+            float nd = -dsum;
+            asm volatile("" : "+v"(nd));  // per block: not hoisted into 16 live registers
+#pragma unroll
+            for (int i = 0; i < 16; ++i) seed[i] = nd;
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < kDqPipe - 1; ++t) read_sd(t);
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
             if (t + kDqPipe - 1 < NSD) read_sd(t + kDqPipe - 1);
             const int c = t & 3, g = t >> 2;
             if (c & 1)
-                dp[c >> 1] = mfma32(opnd[t % kDqPipe], doB[g], g == 0 ? dp_init : dp[c >> 1]);
+                dp[c >> 1] = mfma32(opnd[t % kDqPipe], doB[g], g == 0 ? seed : dp[c >> 1]);
             else
                 s[c >> 1] = mfma32(opnd[t % kDqPipe], qB[g], g == 0 ? zero16() : s[c >> 1]);
             __builtin_amdgcn_sched_barrier(0);
@@ -244,7 +253,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
             for (int r = 0; r < 16; ++r) {
                 float p = exp2_fast(fmaf(s[t][r], cs, -lse2));
                 if constexpr (MASK) p = t * 32 + acc_lrow(r, hh) > lim ? 0.f : p;
-                s[t][r] = HD == 64 ? p * dp[t][r] : p * (dp[t][r] - dsum);
+                s[t][r] = p * dp[t][r];
             }
         f16x8 dsB[4];
 #pragma unroll
