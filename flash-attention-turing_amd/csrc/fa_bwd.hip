@@ -26,7 +26,8 @@
 namespace fa {
 
 constexpr int kBwdThreads = 256;
-// MFMA steps by which the dQ kernel's LDS operand reads run ahead.
+// MFMA steps by which the dQ kernel's LDS operand reads run ahead (head_dim
+// 128; 3 at head_dim 64, whose registers then allow three workgroups per CU).
 constexpr int kDqPipe = 4;
 
 // ---------------------------------------------------------------------------
@@ -81,8 +82,10 @@ struct DqCfg {
 };
 
 template <int HD, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks, const int lg) {
+__global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void bwd_dq_kernel(const fa_bwd_args a, const int num_m_blocks,
+                                                                       const int lg) {
     using C = DqCfg<HD>;
+    constexpr int DQP = HD == 64 ? 3 : kDqPipe;
     constexpr int BM = C::BM, BN = C::BN, NT = C::NT;
     __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
 
@@ -176,15 +179,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
 #pragma unroll
     for (int i = 0; i < HD / 32; ++i) dq[i] = zero16();
     // The dP^T accumulators start from -D (one value per lane: the lane's
-    // query), so dP - D comes out of the MFMAs.  At head_dim 64 the seed tile
-    // is held for the whole kernel; at 128 its 16 registers do not fit there,
-    // so each block fills it just before its dP chains (16 moves instead of
-    // 32 subtractions).
-    f32x16 dp_init = zero16();
-    if constexpr (HD == 64) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dp_init[i] = -dsum;
-    }
+    // query), so dP - D comes out of the MFMAs.  Each block fills that seed
+    // tile just before its dP chains (16 moves instead of 32 subtractions);
+    // held for the whole kernel its 16 registers would not fit at head_dim
+    // 128, nor three workgroups per CU at 64.
 
     TileReader<HD> rd;
     rd.init(lane);
@@ -198,7 +196,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         const int n0 = nb * BN;
         if (CAUSAL && MASK && n0 > q_lo + 31 + causal_off) return;  // no visible key for this wave
         if (q_lo >= sq) return;                                      // no query row of the sequence
-        // Operand reads run kDqPipe - 1 MFMA steps ahead through a ring of
+        // Operand reads run DQP - 1 MFMA steps ahead through a ring of
         // registers, with a scheduling fence per step, so an MFMA does not
         // wait for the LDS read issued just before it.  The lane's read bases
         // get this block's stage added once (opaque, so the per-read
@@ -208,22 +206,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         static_assert(C::STAGE % 512 == 0, "stage offsets must be multiples of 512 bytes");
         int ab = rd.a_base + soff, tb0 = rd.tr_base[0] + soff, tb1 = rd.tr_base[1] + soff;
         asm volatile("" : "+v"(ab), "+v"(tb0), "+v"(tb1));
-        f16x8 opnd[kDqPipe];
+        f16x8 opnd[DQP];
         // S / dP step t: chain c = t % 4 (s[0], dp[0], s[1], dp[1]) at K step
         // g = t / 4, so consecutive MFMAs feed four independent accumulators
         // and each chain still sums g = 0, 1, ... in order.
         constexpr int NSD = 4 * (HD / 16), NDQ = 4 * (HD / 32), NDT = HD / 32;
         auto read_sd = [&](int t) FA_INLINE {
             const int c = t & 3;
-            opnd[t % kDqPipe] = rd.a_operand_at(smem + (c & 1) * C::TILE + 32 * (c >> 1) * (HD * 2), ab, t >> 2);
+            opnd[t % DQP] = rd.a_operand_at(smem + (c & 1) * C::TILE + 32 * (c >> 1) * (HD * 2), ab, t >> 2);
         };
         // dQ step u: accumulator dt = u % NDT at key step gg = u / NDT.
         auto read_dq = [&](int u) FA_INLINE {
-            opnd[u % kDqPipe] = rd.tr_operand_at(smem + 16 * (u / NDT) * (HD * 2), tb0, tb1, u % NDT);
+            opnd[u % DQP] = rd.tr_operand_at(smem + 16 * (u / NDT) * (HD * 2), tb0, tb1, u % NDT);
         };
         f32x16 s[2], dp[2];
-        f32x16 seed = dp_init;
-        if constexpr (HD == 128) {
+        f32x16 seed;
+        {
             float nd = -dsum;
             asm volatile("" : "+v"(nd));  // per block: not hoisted into 16 live registers
 #pragma unroll
@@ -231,21 +229,21 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int t = 0; t < kDqPipe - 1; ++t) read_sd(t);
+        for (int t = 0; t < DQP - 1; ++t) read_sd(t);
 #pragma unroll
         for (int t = 0; t < NSD; ++t) {
-            if (t + kDqPipe - 1 < NSD) read_sd(t + kDqPipe - 1);
+            if (t + DQP - 1 < NSD) read_sd(t + DQP - 1);
             const int c = t & 3, g = t >> 2;
             if (c & 1)
-                dp[c >> 1] = mfma32(opnd[t % kDqPipe], doB[g], g == 0 ? seed : dp[c >> 1]);
+                dp[c >> 1] = mfma32(opnd[t % DQP], doB[g], g == 0 ? seed : dp[c >> 1]);
             else
-                s[c >> 1] = mfma32(opnd[t % kDqPipe], qB[g], g == 0 ? zero16() : s[c >> 1]);
+                s[c >> 1] = mfma32(opnd[t % DQP], qB[g], g == 0 ? zero16() : s[c >> 1]);
             __builtin_amdgcn_sched_barrier(0);
         }
         // The first K^T reads of the dQ product do not depend on dS: they go
         // out before the softmax, which hides their latency.
 #pragma unroll
-        for (int u = 0; u < kDqPipe - 1; ++u) read_dq(u);
+        for (int u = 0; u < DQP - 1; ++u) read_dq(u);
         const int lim = (CAUSAL ? min(sk - 1, qi + causal_off) : sk - 1) - n0;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -261,8 +259,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const fa_bwd_args a, con
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < NDQ; ++u) {
-            if (u + kDqPipe - 1 < NDQ) read_dq(u + kDqPipe - 1);
-            dq[u % NDT] = mfma32(opnd[u % kDqPipe], dsB[u / NDT], dq[u % NDT]);
+            if (u + DQP - 1 < NDQ) read_dq(u + DQP - 1);
+            dq[u % NDT] = mfma32(opnd[u % DQP], dsB[u / NDT], dq[u % NDT]);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
