@@ -476,10 +476,13 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         }
     };
 
-    // The wave's V rows as a read base: the lane's A-operand base plus the rows'
-    // LDS offset.  Every tile offset added to a lane base is a multiple of 512
-    // bytes (TileReader::a_operand_at).
+    // The wave's V rows do not move, so their HD / 16 operand addresses are
+    // formed once and held (the lane's A-operand base plus the rows' LDS
+    // offset, a multiple of 512 bytes, XOR the step: TileReader::a_operand_at).
     const int vb0 = rd0.a_base + 2 * C::STAGE + 32 * kg * (HD * 2);
+    int vaddr[HD / 16];
+#pragma unroll
+    for (int g = 0; g < HD / 16; ++g) vaddr[g] = vb0 ^ (g << 5);
     static_assert(C::STAGE % 512 == 0 && C::QTILE % 512 == 0 && (32 * HD * 2) % 512 == 0,
                   "tile offsets must be multiples of 512 bytes");
 
@@ -494,8 +497,8 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         // where they would hold dozens of registers for the whole kernel); each
         // read is then one XOR (TileReader::a_operand_at / tr_operand_at) and
         // an immediate: Q at 0, dO at QTILE, rows 16.. of a tile at 16 rows.
-        int qb = rd0.a_base + soff, tb0 = rd0.tr_base[0] + soff, tb1 = rd0.tr_base[1] + soff, vb = vb0;
-        asm volatile("" : "+v"(qb), "+v"(tb0), "+v"(tb1), "+v"(vb));
+        int qb = rd0.a_base + soff, tb0 = rd0.tr_base[0] + soff, tb1 = rd0.tr_base[1] + soff;
+        asm volatile("" : "+v"(qb), "+v"(tb0), "+v"(tb1));
         // Operand reads run PIPE steps ahead of the MFMAs that use them, and a
         // scheduling fence after each step keeps that order, so the dK/dV
         // accumulators, the S/dP tiles and the operands in flight fit the
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
         auto ld = [&](int g) {
             qa[g % PIPE] = rd0.a_operand_at(smem, qb, g);
             oa[g % PIPE] = rd0.a_operand_at(smem + C::QTILE, qb, g);
-            va[g % PIPE] = rd0.a_operand_at(smem, vb, g);
+            va[g % PIPE] = lds_ld16(smem, vaddr[g]);
         };
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -531,6 +534,12 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
             dp = mfma32(oa[g % PIPE], va[g % PIPE], dp);
             __builtin_amdgcn_sched_barrier(0);
         }
+        // Masked blocks: accumulator 8 r8 + u holds query qh0 + 8 hh + c with
+        // c = 16 r8 + u, live for m_lo <= c < m_hi (the key at or below the
+        // query's diagonal, the query inside the sequence): two compares with
+        // a constant per element.
+        const int mbase = qh0 + 8 * hh;
+        const int m_lo = CAUSAL ? key - causal_off - mbase : -(1 << 30), m_hi = sq - mbase;
 #pragma unroll
         for (int r8 = 0; r8 < 2; ++r8) {
             const int ql0 = 16 * r8 + 8 * hh;  // rows ql0 + 0..7 for accumulators 8*r8 + 0..7
@@ -542,9 +551,8 @@ __global__ __launch_bounds__(kDkvThreads, 2) void bwd_dkdv_kernel(const fa_bwd_a
                 const float l2 = u < 4 ? l_a[u] : l_b[u - 4];
                 float p = exp2_fast(fmaf(s[r], cs, -l2));
                 if constexpr (MASK) {
-                    const int q = qh0 + 16 * r8 + 8 * hh + u;
-                    const bool dead = q >= sq || (CAUSAL && key > q + causal_off);
-                    p = dead ? 0.f : p;
+                    const int c = 16 * r8 + u;
+                    p = (c < m_lo || c >= m_hi) ? 0.f : p;
                 }
                 s[r] = p;
                 dp[r] = p * dp[r];
