@@ -59,9 +59,9 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 # profiles/hbm_bytes_pmc.md.  Re-measured whenever a kernel changes; None
 # where not measured.
 PMC_TRAFFIC_BYTES = {
-    "fwd": 4.457e8 + 6.899e7,
-    "bwd_dq": 7.454e8 + 6.931e7,
-    "bwd_dkdv": 5.593e8 + 1.519e8,
+    "fwd": 4.624e8 + 6.955e7,
+    "bwd_dq": 1.150e9 + 6.928e7,
+    "bwd_dkdv": 5.586e8 + 1.614e8,
     "kv_splitkv": 4.705e9 + 9.581e6,
 }
 
