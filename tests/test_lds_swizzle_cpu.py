@@ -83,3 +83,49 @@ def test_swizzle_repeats_every_16_rows():
 
 def test_model_sees_the_old_head_dim_64_conflicts():
     assert a_operand_excess(64, old_swz64, 0) > 0
+
+
+def reader_bases(hd, lane):
+    """TileReader<hd>::init: the lane's A-operand base and its two transposed-read bases."""
+    kch, rowb = hd // 8, hd * 2
+    col, h = lane & 31, lane >> 5
+    row = sigma(col)
+    a_base = row * rowb + (((h ^ swz(kch, row)) & (kch - 1)) << 4)
+    j, q, db = (lane & 15) >> 2, lane & 3, (lane >> 4) & 1
+    x, byte = 2 * db + (q >> 1), (q & 1) * 8
+    tr = [(8 * h + j + 4 * hs) * rowb + (((x ^ swz(kch, 8 * h + j + 4 * hs)) & (kch - 1)) << 4) + byte
+          for hs in range(2)]
+    return a_base, tr
+
+
+def tile_offsets(hd):
+    """Every tile offset the kernels add to a lane base once (a_operand_at / tr_operand_at):
+    the dK/dV stages and the wave's V rows, the dQ and forward stages."""
+    dkv_qtile = 32 * hd * 2
+    dkv_stage = 2 * dkv_qtile + 2 * 64 * 4
+    offs = {0, dkv_stage} | {2 * dkv_stage + kg * 32 * hd * 2 for kg in range(4)}
+    kv_stage = 2 * (64 * hd * 2)  # dQ and forward: a K and a V tile of 64 keys
+    return offs | {kv_stage}
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_tile_offset_commutes_with_step_xor(hd):
+    """The kernels form base + t once per tile and read at (base + t) ^ m for the step mask
+    m (g << 5, dt << 6); that address must be the per-read form (base ^ m) + t, for every
+    lane base, tile offset and step."""
+    masks = [g << 5 for g in range(hd // 16)] + [dt << 6 for dt in range(hd // 32)]
+    for t in tile_offsets(hd):
+        assert t % 512 == 0
+        for lane in range(64):
+            a_base, tr = reader_bases(hd, lane)
+            for base in (a_base, *tr):
+                for m in masks:
+                    assert (base + t) ^ m == (base ^ m) + t
+
+
+def test_commuting_needs_the_offset_alignment():
+    """The identity needs the offset's bits up to the highest step bit (bit 7) clear; 512 is
+    what the kernels assert.  A plausible slip, an offset inside a row (here two 16-byte
+    chunks), breaks it for some lane and step, so the check above can fail."""
+    assert any((base + 32) ^ (g << 5) != (base ^ (g << 5)) + 32
+               for lane in range(64) for base in (reader_bases(128, lane)[0],) for g in range(8))
